@@ -1,0 +1,163 @@
+/*
+ * qattn.h -- C ABI of the MI355X (gfx950) ancestor-sparse tree-verify
+ * attention library, libqattn.so.
+ *
+ * Every entry point takes plain device pointers, element strides and sizes,
+ * launches asynchronously on the given HIP stream (hipStream_t passed as
+ * void*, NULL = the legacy default stream), allocates nothing and keeps no
+ * global mutable state, so calls are reentrant and HIP-graph capturable.
+ * Return value: QATTN_OK (0) or a negative QATTN_ERR_* code; the message of
+ * the last failure on the calling thread is qattn_last_error().
+ *
+ * Conventions shared by the entry points
+ *   - Tensors are [tokens, heads, head_dim] with strides given as
+ *     {stride_token, stride_head, stride_dim} in ELEMENTS; stride_dim must be
+ *     1 and every row must start on a 16-byte boundary (else
+ *     QATTN_ERR_LAYOUT; callers copy to a contiguous layout).
+ *   - dtype is QATTN_DTYPE_F16 or QATTN_DTYPE_BF16 for q, k, v and o alike;
+ *     arithmetic is fp32; o is rounded once (nearest even).
+ *   - head_dim is 32, 64 or 128.  num_q_heads must be a multiple of
+ *     num_kv_heads (GQA: q head h reads kv head h / (num_q_heads/num_kv_heads),
+ *     the mapping of repeat_kv; num_kv_heads == num_q_heads is the reference
+ *     layout).
+ *   - cu_seqlens is a DEVICE int32 array [batch + 1] of sequence offsets;
+ *     max_seqlen bounds every sequence length (tokens at or beyond it are not
+ *     computed).  A sequence whose offsets are decreasing, negative or beyond
+ *     total_tokens is skipped (its output rows are left untouched).
+ *   - scale multiplies q.k (the reference fixes it to 1/sqrt(head_dim)).
+ *   - lse (optional, may be NULL) is fp32 [tokens, num_q_heads] with strides
+ *     {stride_token, stride_head}: lse = m + ln(sum exp(s - m)).
+ */
+#ifndef QATTN_H_
+#define QATTN_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define QATTN_OK 0
+#define QATTN_ERR_ARG (-1)       /* null pointer, bad size or inconsistent shape */
+#define QATTN_ERR_DTYPE (-2)     /* dtype not fp16/bf16 */
+#define QATTN_ERR_HEAD_DIM (-3)  /* head_dim not in {32, 64, 128} */
+#define QATTN_ERR_LAYOUT (-4)    /* stride_dim != 1 or a row not 16-byte aligned */
+#define QATTN_ERR_WORKSPACE (-5) /* workspace missing or too small */
+#define QATTN_ERR_HIP (-6)       /* HIP launch/runtime error */
+
+#define QATTN_DTYPE_F16 0
+#define QATTN_DTYPE_BF16 1
+
+/* Kernel selection for qattn_tree_fwd (QATTN_ALGO_AUTO picks per shape). */
+#define QATTN_ALGO_AUTO 0
+#define QATTN_ALGO_GATHER 1  /* one row group per (token, head), gathers from global */
+#define QATTN_ALGO_SUBTREE 2 /* subtree tiles staged in LDS (heap trees only) */
+
+/* Library version string. */
+const char *qattn_version(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char *qattn_last_error(void);
+
+/*
+ * Ancestor-sparse attention over complete b-ary heap-indexed trees.
+ *
+ * Replaces _ragged_attn_sparse_kernel / _ragged_attn_sparse_kernel_lse /
+ * _ragged_attn_sibling_kernel(_lse) (src/ragged_attn.py:262-497, 1206-1420)
+ * as launched by ragged_attention (:1080-1166), ragged_attention_with_lse
+ * (:499-572) and the sibling wrappers (:1423-1556).
+ *
+ * For token t of sequence s (local index x = t - cu[s]) and q head h:
+ *   A(x) = { c_i : c_0 = x, c_{i+1} = max(c_i - 1, 0) / b, c_i != c_{i-1},
+ *            i = 0..max_depth }
+ *   o[t,h] = softmax_{a in A(x)}(scale q[t,h].k[cu[s]+a,kvh]) . v[cu[s]+a,kvh]
+ */
+int qattn_tree_fwd(const void *q, const int64_t q_stride[3],
+                   const void *k, const int64_t k_stride[3],
+                   const void *v, const int64_t v_stride[3],
+                   void *o, const int64_t o_stride[3],
+                   float *lse, const int64_t lse_stride[2],
+                   const int32_t *cu_seqlens, int32_t batch, int32_t max_seqlen,
+                   int64_t total_tokens, int32_t num_q_heads, int32_t num_kv_heads,
+                   int32_t head_dim, int32_t branching_factor, int32_t max_depth,
+                   float scale, int32_t dtype, int32_t algo, void *stream);
+
+/*
+ * Ancestor-sparse attention with an explicit parent array (irregular trees).
+ *
+ * Replaces _ragged_attn_parents_kernel_lse (src/ragged_attn.py:588-714)
+ * launched by ragged_attention_with_parents (:716-795).  parents is a DEVICE
+ * int32 array [total_tokens] of sequence-local parent indices; a root must
+ * self-loop (parents[root] == root).  The walk is c_{i+1} = parents[cu[s]+c_i],
+ * attending c_i iff c_i != c_{i-1}, for i = 0..max_depth.  A parent outside
+ * [0, sequence length) ends the walk (the reference leaves it undefined).
+ */
+int qattn_tree_parents_fwd(const void *q, const int64_t q_stride[3],
+                           const void *k, const int64_t k_stride[3],
+                           const void *v, const int64_t v_stride[3],
+                           void *o, const int64_t o_stride[3],
+                           float *lse, const int64_t lse_stride[2],
+                           const int32_t *cu_seqlens, const int32_t *parents,
+                           int32_t batch, int32_t max_seqlen, int64_t total_tokens,
+                           int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                           int32_t max_depth, float scale, int32_t dtype, void *stream);
+
+/*
+ * Ancestor-sparse attention reading K/V from a paged cache.
+ *
+ * Replaces _ragged_attn_paged_kernel (src/ragged_attn.py:822-929) launched by
+ * ragged_attention_paged (:932-1003).  k_cache / v_cache are
+ * [num_pages, page_size, num_kv_heads, head_dim] with strides
+ * {page, slot, head, dim}; page_table is a DEVICE int32 [batch, pt_cols]
+ * array (row stride pt_cols).  Ancestor position c of sequence s lives at
+ * page page_table[s, c / page_size], slot c % page_size.  A page index outside
+ * [0, num_pages) or a logical page beyond pt_cols skips that ancestor.
+ */
+int qattn_tree_paged_fwd(const void *q, const int64_t q_stride[3],
+                         const void *k_cache, const int64_t k_stride[4],
+                         const void *v_cache, const int64_t v_stride[4],
+                         void *o, const int64_t o_stride[3],
+                         float *lse, const int64_t lse_stride[2],
+                         const int32_t *cu_seqlens, const int32_t *page_table,
+                         int32_t pt_cols, int32_t num_pages, int32_t page_size,
+                         int32_t batch, int32_t max_seqlen, int64_t total_tokens,
+                         int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                         int32_t branching_factor, int32_t max_depth, float scale,
+                         int32_t dtype, void *stream);
+
+/*
+ * Ancestor index table of the heap walk (parents == NULL) or the
+ * explicit-parent walk, computed by the same device code as the attention
+ * kernels.  out is a DEVICE int32 [total_tokens, max_depth + 1] array:
+ * out[t, i] = c_i if step i attends, else -1.  No reference counterpart as an
+ * entry point: it exposes the walk of src/ragged_attn.py:323-377 / :650-698
+ * so index sets can be checked bit-exactly.
+ */
+int qattn_ancestors(const int32_t *cu_seqlens, const int32_t *parents, int32_t batch,
+                    int32_t max_seqlen, int64_t total_tokens, int32_t branching_factor,
+                    int32_t max_depth, int32_t *out, void *stream);
+
+/*
+ * Two-state softmax merge.
+ *
+ * Replaces _fused_lse_merge_kernel (src/ragged_attn.py:1575-1616) launched by
+ * fused_lse_merge (:1619-1653):
+ *   w_p = exp(lse_p - max), w_t = exp(lse_t - max),
+ *   out = (w_p o_p + w_t o_t) / max(w_p + w_t, 1e-8).
+ * o_pre, o_tree, out are [B, H, Nq, D] with 4 element strides each (any
+ * layout with stride_dim 1 and 16-byte aligned rows); lse_pre, lse_tree are
+ * fp32 [B, H, Nq] with 3 strides each.
+ */
+int qattn_lse_merge(const float *lse_pre, const int64_t lse_pre_stride[3],
+                    const float *lse_tree, const int64_t lse_tree_stride[3],
+                    const void *o_pre, const int64_t o_pre_stride[4],
+                    const void *o_tree, const int64_t o_tree_stride[4],
+                    void *out, const int64_t out_stride[4],
+                    int32_t B, int32_t H, int32_t Nq, int32_t head_dim,
+                    int32_t dtype, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QATTN_H_ */

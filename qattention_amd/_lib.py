@@ -1,0 +1,94 @@
+"""ctypes binding of libqattn.so (the C ABI declared in include/qattn.h).
+
+The library must be built in-tree (python -m qattention_amd.build).  There is
+no fallback: if it is missing, every call raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import torch  # noqa: F401  -- must be loaded first so libqattn.so binds torch's HIP runtime
+
+from .build import LIB_PATH
+
+QATTN_OK = 0
+ERRORS = {
+    -1: "QATTN_ERR_ARG",
+    -2: "QATTN_ERR_DTYPE",
+    -3: "QATTN_ERR_HEAD_DIM",
+    -4: "QATTN_ERR_LAYOUT",
+    -5: "QATTN_ERR_WORKSPACE",
+    -6: "QATTN_ERR_HIP",
+}
+QATTN_ERR_LAYOUT = -4
+
+DTYPE_F16 = 0
+DTYPE_BF16 = 1
+ALGO_AUTO, ALGO_GATHER, ALGO_SUBTREE = 0, 1, 2
+
+# Every symbol declared in include/qattn.h, with its ctypes signature.
+_p = C.c_void_p
+_i32 = C.c_int32
+_i64 = C.c_int64
+_f32 = C.c_float
+_i64p = C.POINTER(C.c_int64)
+
+SIGNATURES = {
+    "qattn_version": (C.c_char_p, []),
+    "qattn_last_error": (C.c_char_p, []),
+    "qattn_tree_fwd": (C.c_int, [
+        _p, _i64p, _p, _i64p, _p, _i64p, _p, _i64p, _p, _i64p,
+        _p, _i32, _i32, _i64, _i32, _i32, _i32, _i32, _i32, _f32, _i32, _i32, _p]),
+    "qattn_tree_parents_fwd": (C.c_int, [
+        _p, _i64p, _p, _i64p, _p, _i64p, _p, _i64p, _p, _i64p,
+        _p, _p, _i32, _i32, _i64, _i32, _i32, _i32, _i32, _f32, _i32, _p]),
+    "qattn_tree_paged_fwd": (C.c_int, [
+        _p, _i64p, _p, _i64p, _p, _i64p, _p, _i64p, _p, _i64p,
+        _p, _p, _i32, _i32, _i32, _i32, _i32, _i64, _i32, _i32, _i32, _i32, _i32, _f32, _i32, _p]),
+    "qattn_ancestors": (C.c_int, [_p, _p, _i32, _i32, _i64, _i32, _i32, _p, _p]),
+    "qattn_lse_merge": (C.c_int, [
+        _p, _i64p, _p, _i64p, _p, _i64p, _p, _i64p, _p, _i64p,
+        _i32, _i32, _i32, _i32, _i32, _p]),
+}
+
+_lib = None
+
+
+class QAttnError(RuntimeError):
+    pass
+
+
+def lib():
+    """Load libqattn.so once; raise if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise QAttnError(
+                f"{LIB_PATH} is missing: build it with `python -m qattention_amd.build` "
+                "(or __graft_entry__.build()); there is no non-HIP fallback")
+        L = C.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def last_error() -> str:
+    return lib().qattn_last_error().decode(errors="replace")
+
+
+def check(rc: int, what: str) -> None:
+    if rc != QATTN_OK:
+        raise QAttnError(f"{what} failed: {ERRORS.get(rc, rc)}: {last_error()}")
+
+
+def i64arr(vals):
+    arr = (C.c_int64 * len(vals))(*[int(x) for x in vals])
+    return arr
+
+
+def ptr(t) -> int:
+    return 0 if t is None else t.data_ptr()

@@ -1,0 +1,98 @@
+// qattn_common.h -- host/device shared definitions: parameter blocks, the
+// heap-walk divider, the subtree tiling plan and error reporting.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/qattn.h"
+
+namespace qattn {
+
+// ---------------------------------------------------------------------------
+// Division by the branching factor.  The heap walk needs
+// parent(c) = max(c - 1, 0) / b  (src/ragged_attn.py:376-377, clamp before the
+// divide).  b is a launch constant, so the divide becomes a multiply-high:
+// with l = ceil(log2 b) and m = floor(2^32 (2^l - b) / b) + 1,
+// x / b = (mulhi(x, m) + x) >> l for every 0 <= x < 2^31.
+// ---------------------------------------------------------------------------
+struct Divider {
+    uint32_t magic;
+    int32_t shift;
+    int32_t d;
+};
+
+inline Divider make_divider(int32_t d) {
+    Divider r;
+    r.d = d;
+    int l = 0;
+    while ((int64_t(1) << l) < d) ++l;
+    r.shift = l;
+    uint64_t num = (uint64_t(1) << 32) * ((uint64_t(1) << l) - uint64_t(d));
+    r.magic = uint32_t(num / uint64_t(d) + 1);
+    return r;
+}
+
+__device__ __forceinline__ int32_t divide(int32_t x, const Divider& dv) {
+    uint32_t ux = uint32_t(x);
+    uint32_t hi = __umulhi(ux, dv.magic);
+    return int32_t((hi + ux) >> dv.shift);
+}
+
+// One step of the heap ancestor walk: max(c - 1, 0) / b.
+__device__ __forceinline__ int32_t heap_parent(int32_t c, const Divider& dv) {
+    int32_t m = c - 1;
+    m = m > 0 ? m : 0;
+    return divide(m, dv);
+}
+
+// ---------------------------------------------------------------------------
+// Parameter block of the tree kernels (passed by value as a kernel argument).
+// Strides are in elements; the d-stride of every tensor is 1.
+// ---------------------------------------------------------------------------
+struct TreeParams {
+    const void* q;
+    const void* k;
+    const void* v;
+    void* o;
+    float* lse;
+    const int32_t* cu;          // [B+1] sequence offsets into q/o (and packed k/v)
+    const int32_t* parents;     // explicit-parent walk: sequence-local parent per token
+    const int32_t* page_table;  // paged K/V: [B, pt_cols] physical page per logical page
+    int64_t sq_t, sq_h, sk_t, sk_h, sv_t, sv_h, so_t, so_h;
+    int64_t slse_t, slse_h;
+    int64_t sk_page, sv_page;   // paged K/V: elements between pages (sk_t/sv_t = slot stride)
+    int64_t total_tokens;       // rows of q / o
+    int64_t kv_rows;            // rows of packed k / v
+    int32_t num_pages, pt_cols, page_size;
+    int32_t B, Hq, Hkv, group, max_seqlen, max_depth;
+    Divider bdiv;               // branching factor
+    float scale_log2;           // softmax scale * log2(e)
+    // split-K prefix partial state merged into the tree state (may be null)
+    const float* part_m;        // [n_split][T][Hq]   running max (log2 domain)
+    const float* part_l;        // [n_split][T][Hq]   running denominator
+    const float* part_acc;      // [n_split][T][Hq][D] unnormalised numerator
+    int32_t n_split;
+    // tree K/V location of sequence `seq` is cu[seq] + kv_seq_off * seq
+    // (0 for the packed layout; the hybrid layout places L prefix rows before
+    // every sequence's tree rows).
+    int64_t kv_row0;            // extra row offset before the tree rows of each sequence
+    int64_t kv_seq_stride;      // rows between consecutive sequences in k/v (0: use cu)
+};
+
+// Subtree tiling of a heap-indexed tree (levels of the BFS order).
+constexpr int kMaxBands = 32;
+struct Band {
+    int32_t lo, hi, G, tile_base;
+};
+struct SubtreePlan {
+    int32_t nbands;
+    int32_t total_tiles;
+    int32_t max_rows;     // LDS rows (K and V each) of the largest tile
+    int32_t chain_h;      // b == 1: levels per tile
+    Band band[kMaxBands];
+};
+
+void set_error(const char* fmt, ...);
+
+}  // namespace qattn

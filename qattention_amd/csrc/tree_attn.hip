@@ -1,0 +1,958 @@
+// tree_attn.hip -- ancestor-sparse tree-verify attention kernels for gfx950.
+//
+// Two kernels compute the same function (the ancestor walk + softmax of
+// src/ragged_attn.py:262-497):
+//
+//  * tree_gather_kernel   one row group (D/8 lanes, 16 B per lane) per
+//                         (token, q head); the d+1 ancestor rows of a chunk of
+//                         steps are gathered from global memory with all loads
+//                         issued before the first score is formed.  Handles the
+//                         heap walk, the explicit-parent walk and the paged
+//                         K/V layout, and merges split-K prefix partial states.
+//
+//  * tree_subtree_kernel  heap trees only.  A workgroup owns one subtree tile
+//                         (a band of BFS levels under G adjacent roots) of one
+//                         (sequence, kv head).  It stages the tile's K/V rows and
+//                         the few ancestor rows above it in LDS once, so every
+//                         ancestor read of every query in the tile is an LDS
+//                         read and each K/V row leaves HBM once per kv head.
+//                         All q heads of a GQA group share the staged rows.
+//
+// Scores are kept in the log2 domain (scale * log2(e) folded into one multiply)
+// and exponentiated with v_exp_f32.  Dot products use v_dot2_f32_{f16,bf16};
+// the D/8-lane reduction uses DPP.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include <algorithm>
+#include <vector>
+
+#include "qattn_common.h"
+#include "qattn_device.h"
+
+namespace qattn {
+
+constexpr int kThreads = 256;
+constexpr int kChunk = 8;          // ancestor steps whose loads are issued together
+constexpr int kLdsBudget = 48 * 1024;  // bytes of K+V rows staged per subtree tile
+constexpr int kMaxPass = 6;        // staging passes (kLdsBudget / (4 D) rows / (256 / (D/8)))
+
+enum { WALK_HEAP = 0, WALK_PARENTS = 1 };
+enum { KV_PACKED = 0, KV_PAGED = 1 };
+
+static thread_local char g_err[512];
+
+void set_error(const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+}
+
+// ---------------------------------------------------------------------------
+// Device helpers shared by the kernels
+// ---------------------------------------------------------------------------
+
+// Sequence bounds with the guards documented in qattn.h.
+__device__ __forceinline__ bool seq_bounds(const TreeParams& p, int seq, int32_t& start, int32_t& n) {
+    int32_t s = p.cu[seq], e = p.cu[seq + 1];
+    if (s < 0 || e < s || (int64_t)e > p.total_tokens) return false;
+    start = s;
+    n = e - s;
+    if (n > p.max_seqlen) n = p.max_seqlen;
+    return true;
+}
+
+__device__ __forceinline__ int64_t kv_base(const TreeParams& p, int seq, int32_t start) {
+    return p.kv_seq_stride ? (int64_t)seq * p.kv_seq_stride + p.kv_row0 : (int64_t)start;
+}
+
+// Next node of the walk (src/ragged_attn.py:376-377 heap, :692-694 parents).
+template <int WALK>
+__device__ __forceinline__ int32_t walk_next(const TreeParams& p, int32_t start, int32_t n, int32_t cur) {
+    if constexpr (WALK == WALK_HEAP) {
+        return heap_parent(cur, p.bdiv);
+    } else {
+        int32_t par = p.parents[start + cur];
+        return (par >= 0 && par < n) ? par : cur;
+    }
+}
+
+// Initial softmax state from split-K prefix partials (flash-decoding merge).
+template <int D>
+__device__ __forceinline__ void load_partial_state(const TreeParams& p, int64_t qrow, int h, int lane,
+                                                   float& m, float& l, float* acc) {
+    const int64_t plane = p.total_tokens * (int64_t)p.Hq;
+    const int64_t idx = qrow * p.Hq + h;
+    float m0 = -INFINITY;
+    for (int s = 0; s < p.n_split; ++s) m0 = fmaxf(m0, p.part_m[s * plane + idx]);
+    m = m0;
+    l = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] = 0.f;
+    if (m0 == -INFINITY) return;
+    for (int s = 0; s < p.n_split; ++s) {
+        const float w = fast_exp2(p.part_m[s * plane + idx] - m0);
+        l = __builtin_fmaf(w, p.part_l[s * plane + idx], l);
+        const float4* a = reinterpret_cast<const float4*>(p.part_acc + (s * plane + idx) * D + lane * 8);
+        float4 a0 = a[0], a1 = a[1];
+        acc[0] = __builtin_fmaf(w, a0.x, acc[0]);
+        acc[1] = __builtin_fmaf(w, a0.y, acc[1]);
+        acc[2] = __builtin_fmaf(w, a0.z, acc[2]);
+        acc[3] = __builtin_fmaf(w, a0.w, acc[3]);
+        acc[4] = __builtin_fmaf(w, a1.x, acc[4]);
+        acc[5] = __builtin_fmaf(w, a1.y, acc[5]);
+        acc[6] = __builtin_fmaf(w, a1.z, acc[6]);
+        acc[7] = __builtin_fmaf(w, a1.w, acc[7]);
+    }
+}
+
+// Fold one chunk of scores (log2 domain, -inf = not attended) into (m, l, acc).
+template <typename T, int CH>
+__device__ __forceinline__ void softmax_fold(float& m, float& l, float* acc, const float* sc, const Vec16* vr) {
+    float cmax = sc[0];
+#pragma unroll
+    for (int j = 1; j < CH; ++j) cmax = fmaxf(cmax, sc[j]);
+    const float m_new = fmaxf(m, cmax);
+    const float m_ref = (m_new == -INFINITY) ? 0.f : m_new;
+    const float alpha = fast_exp2(m - m_ref);
+    l *= alpha;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] *= alpha;
+#pragma unroll
+    for (int j = 0; j < CH; ++j) {
+        const float pj = fast_exp2(sc[j] - m_ref);  // exp2(-inf) = 0 for skipped steps
+        l += pj;
+        axpy8<T>(acc, pj, vr[j]);
+    }
+    m = m_new;
+}
+
+// Normalise and write one output row group (+ LSE from lane 0).
+template <typename T, bool LSE>
+__device__ __forceinline__ void write_out(const TreeParams& p, int64_t qrow, int h, int lane,
+                                          float m, float l, float* acc) {
+    // l == 0 only for a query with no attended key; the reference divides by 1
+    // there (src/ragged_attn.py:379-380).
+    const float l_safe = (l == 0.f) ? 1.f : l;
+    const float inv = __builtin_amdgcn_rcpf(l_safe);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] *= inv;
+    uint16_t* optr = (uint16_t*)p.o + qrow * p.so_t + (int64_t)h * p.so_h + lane * 8;
+    st16(optr, pack8<T>(acc));
+    if constexpr (LSE) {
+        if (lane == 0) p.lse[qrow * p.slse_t + (int64_t)h * p.slse_h] = (m + fast_log2(l_safe)) * kLn2;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Gather kernel
+// ---------------------------------------------------------------------------
+template <typename T, int D, int WALK, int LAYOUT, bool LSE, bool PSTATE>
+__global__ __launch_bounds__(kThreads) void tree_gather_kernel(TreeParams p) {
+    constexpr int LPR = D / 8;
+    constexpr int SLOTS = kThreads / LPR;
+    const int lane = threadIdx.x % LPR;
+    const int64_t slot = (int64_t)blockIdx.x * SLOTS + threadIdx.x / LPR;
+    const int h = (int)(slot % p.Hq);
+    const int64_t rest = slot / p.Hq;
+    const int tok = (int)(rest % p.max_seqlen);
+    const int seq = (int)(rest / p.max_seqlen);
+    if (seq >= p.B) return;
+    int32_t start, n;
+    if (!seq_bounds(p, seq, start, n)) return;
+    if (tok >= n) return;
+    const int kvh = h / p.group;
+    const int64_t kvb = kv_base(p, seq, start);
+    const int64_t qrow = (int64_t)start + tok;
+
+    const uint16_t* kbase = (const uint16_t*)p.k + (int64_t)kvh * p.sk_h + lane * 8;
+    const uint16_t* vbase = (const uint16_t*)p.v + (int64_t)kvh * p.sv_h + lane * 8;
+    const Vec16 qv = ld16((const uint16_t*)p.q + qrow * p.sq_t + (int64_t)h * p.sq_h + lane * 8);
+
+    float m = -INFINITY, l = 0.f, acc[8];
+    if constexpr (PSTATE) {
+        load_partial_state<D>(p, qrow, h, lane, m, l, acc);
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[j] = 0.f;
+    }
+
+    int32_t cur = tok, prev = -1;
+    for (int s0 = 0; s0 <= p.max_depth; s0 += kChunk) {
+        int64_t koff[kChunk], voff[kChunk];
+        bool val[kChunk];
+#pragma unroll
+        for (int j = 0; j < kChunk; ++j) {
+            bool ok = (s0 + j <= p.max_depth) && (cur != prev);
+            int64_t ko = 0, vo = 0;
+            if constexpr (LAYOUT == KV_PACKED) {
+                const int64_t row = kvb + cur;
+                ko = row * p.sk_t;
+                vo = row * p.sv_t;
+            } else {
+                const int32_t lp = cur / p.page_size;
+                const int32_t sl = cur - lp * p.page_size;
+                int32_t pg = -1;
+                if (ok && lp < p.pt_cols) pg = p.page_table[(int64_t)seq * p.pt_cols + lp];
+                ok = ok && pg >= 0 && pg < p.num_pages;
+                ko = (int64_t)pg * p.sk_page + (int64_t)sl * p.sk_t;
+                vo = (int64_t)pg * p.sv_page + (int64_t)sl * p.sv_t;
+            }
+            val[j] = ok;
+            koff[j] = ko;
+            voff[j] = vo;
+            prev = cur;
+            cur = walk_next<WALK>(p, start, n, cur);
+        }
+        Vec16 kr[kChunk], vr[kChunk];
+#pragma unroll
+        for (int j = 0; j < kChunk; ++j) {
+            kr[j] = Vec16{{0u, 0u, 0u, 0u}};
+            vr[j] = Vec16{{0u, 0u, 0u, 0u}};
+            if (val[j]) {
+                kr[j] = ld16(kbase + koff[j]);
+                vr[j] = ld16(vbase + voff[j]);
+            }
+        }
+        float sc[kChunk];
+#pragma unroll
+        for (int j = 0; j < kChunk; ++j) {
+            const float d = group_sum<LPR>(dot8<T>(qv, kr[j])) * p.scale_log2;
+            sc[j] = val[j] ? d : -INFINITY;
+        }
+        softmax_fold<T, kChunk>(m, l, acc, sc, vr);
+        // The walk is stalled (root reached / self-loop) for every lane.
+        if (!__any(cur != prev)) break;
+    }
+    write_out<T, LSE>(p, qrow, h, lane, m, l, acc);
+}
+
+// ---------------------------------------------------------------------------
+// Subtree kernel (heap walk, packed or hybrid K/V layout)
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int rl(int v, int i) { return __builtin_amdgcn_readlane(v, i); }
+
+template <typename T, int D, bool LSE, bool PSTATE>
+__global__ __launch_bounds__(kThreads) void tree_subtree_kernel(TreeParams p, SubtreePlan plan, Divider gdiv) {
+    constexpr int LPR = D / 8;
+    constexpr int SLOTS = kThreads / LPR;  // row groups per workgroup
+    extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
+    uint16_t* Ks = smem;
+    uint16_t* Vs = smem + (size_t)plan.max_rows * D;
+
+    const int lane = threadIdx.x % LPR;
+    const int rg = threadIdx.x / LPR;
+    const int lane64 = threadIdx.x & 63;
+
+    const int kvh = blockIdx.x % p.Hkv;
+    const int rest = blockIdx.x / p.Hkv;
+    const int tile = rest % plan.total_tiles;
+    const int seq = rest / plan.total_tiles;
+    if (seq >= p.B) return;
+    int32_t start, n;
+    if (!seq_bounds(p, seq, start, n)) return;
+    if (n <= 0) return;
+    const int b = p.bdiv.d;
+
+    // ---- which band / roots ------------------------------------------------
+    int lo = 0, hi = 0, G = 1, tbase = 0;
+#pragma unroll
+    for (int i = 0; i < kMaxBands; ++i) {
+        if (i < plan.nbands && tile >= plan.band[i].tile_base) {
+            lo = plan.band[i].lo;
+            hi = plan.band[i].hi;
+            G = plan.band[i].G;
+            tbase = plan.band[i].tile_base;
+        }
+    }
+    int64_t r0, r1;  // root range [r0, r1) at level lo
+    if (b == 1) {
+        lo = (tile - tbase) * plan.chain_h;
+        hi = lo + plan.chain_h - 1;
+        r0 = lo;
+        r1 = lo + 1;
+    } else {
+        int64_t s_lo = 0, w_lo = 1;
+        for (int i = 0; i < lo; ++i) {
+            s_lo += w_lo;
+            w_lo *= b;
+        }
+        const int64_t i0 = (int64_t)(tile - tbase) * G;
+        r0 = s_lo + i0;
+        r1 = s_lo + ((i0 + G < w_lo) ? i0 + G : w_lo);
+    }
+    if (r0 >= n) return;
+    if (r1 > n) r1 = n;
+
+    // ---- level table, one level per lane (lane 0 = level lam_min) ----------
+    const int lam_min = (lo - p.max_depth > 0) ? lo - p.max_depth : 0;
+    const int nlev = hi - lam_min + 1;  // <= 64, guaranteed by the host plan
+    int first = 0, cnt = 0;
+    if (lane64 < nlev) {
+        const int lam = lam_min + lane64;
+        int64_t f, la;
+        if (lam >= lo) {
+            const int j = lam - lo;
+            int64_t bj = 1, sj = 0;
+            for (int i = 0; i < j; ++i) {
+                sj += bj;
+                bj *= b;
+            }
+            f = r0 * bj + sj;
+            la = r1 * bj + sj - 1;
+        } else {
+            int32_t a = (int32_t)r0, c = (int32_t)(r1 - 1);
+            for (int i = 0; i < lo - lam; ++i) {
+                a = heap_parent(a, p.bdiv);
+                c = heap_parent(c, p.bdiv);
+            }
+            f = a;
+            la = c;
+        }
+        if (la > n - 1) la = n - 1;
+        if (f <= la) {
+            first = (int)f;
+            cnt = (int)(la - f + 1);
+        }
+    }
+    int base = 0;
+    for (int i = 0; i < nlev; ++i) {
+        const int c = rl(cnt, i);
+        base += (i < lane64) ? c : 0;
+    }
+    const int off = base - first;  // LDS row of node x at this level = x + off
+    const int total_rows = rl(base + cnt, nlev - 1);
+    if (total_rows > plan.max_rows) return;  // cannot happen for a host-built plan
+
+    const int64_t kvb = kv_base(p, seq, start);
+    const uint16_t* kg = (const uint16_t*)p.k + (int64_t)kvh * p.sk_h + lane * 8;
+    const uint16_t* vg = (const uint16_t*)p.v + (int64_t)kvh * p.sv_h + lane * 8;
+
+    // ---- stage K/V rows: all global loads issued before the first LDS write --
+    Vec16 kst[kMaxPass], vst[kMaxPass];
+    int offr[kMaxPass];
+#pragma unroll
+    for (int ps = 0; ps < kMaxPass; ++ps) offr[ps] = rl(off, 0);
+    for (int i = 1; i < nlev; ++i) {
+        const int bi = rl(base, i), oi = rl(off, i), ci = rl(cnt, i);
+#pragma unroll
+        for (int ps = 0; ps < kMaxPass; ++ps) {
+            const int r = ps * SLOTS + rg;
+            if (ci > 0 && r >= bi) offr[ps] = oi;
+        }
+    }
+#pragma unroll
+    for (int ps = 0; ps < kMaxPass; ++ps) {
+        const int r = ps * SLOTS + rg;
+        if (r < total_rows) {
+            const int64_t row = kvb + (r - offr[ps]);
+            kst[ps] = ld16(kg + row * p.sk_t);
+            vst[ps] = ld16(vg + row * p.sv_t);
+        }
+    }
+
+    // ---- query cursor: levels lo..hi, SLOTS (node, q head) pairs per pass ---
+    const int g = p.group;
+    int lam = lo, s0 = 0;
+    auto level_items = [&](int L) -> int { return (L <= hi) ? rl(cnt, L - lam_min) * g : 0; };
+    auto load_q = [&](int L, int s, Vec16& dst) {
+        const int node = rl(first, L - lam_min) + divide(s, gdiv);
+        const int qh = kvh * g + (s - divide(s, gdiv) * g);
+        dst = ld16((const uint16_t*)p.q + ((int64_t)start + node) * p.sq_t + (int64_t)qh * p.sq_h + lane * 8);
+    };
+    Vec16 qcur = Vec16{{0u, 0u, 0u, 0u}}, qnext = Vec16{{0u, 0u, 0u, 0u}};
+    int items = level_items(lam);
+    if (rg < items) load_q(lam, rg, qcur);
+
+#pragma unroll
+    for (int ps = 0; ps < kMaxPass; ++ps) {
+        const int r = ps * SLOTS + rg;
+        if (r < total_rows) {
+            st16(Ks + (size_t)r * D + lane * 8, kst[ps]);
+            st16(Vs + (size_t)r * D + lane * 8, vst[ps]);
+        }
+    }
+    __syncthreads();
+
+    while (lam <= hi && items > 0) {
+        // next cursor position and its Q prefetch
+        int lam_n = lam, s0_n = s0 + SLOTS, items_n = items;
+        if (s0_n >= items) {
+            lam_n = lam + 1;
+            s0_n = 0;
+            items_n = level_items(lam_n);
+        }
+        if (s0_n + rg < items_n) load_q(lam_n, s0_n + rg, qnext);
+
+        const int s = s0 + rg;
+        if (s < items) {
+            const int node = rl(first, lam - lam_min) + divide(s, gdiv);
+            const int qh = kvh * g + (s - divide(s, gdiv) * g);
+            const int64_t qrow = (int64_t)start + node;
+            float m = -INFINITY, l = 0.f, acc[8];
+            if constexpr (PSTATE) {
+                load_partial_state<D>(p, qrow, qh, lane, m, l, acc);
+            } else {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) acc[j] = 0.f;
+            }
+            // steps t = 0..min(lam, max_depth) attend levels lam - t; the heap
+            // walk strictly decreases until the root, so these are exactly the
+            // steps with c_t != c_{t-1} (src/ragged_attn.py:338-377).
+            const int nsteps = (lam < p.max_depth ? lam : p.max_depth) + 1;
+            int32_t cur = node;
+            for (int t0 = 0; t0 < nsteps; t0 += kChunk) {
+                Vec16 kr[kChunk], vr[kChunk];
+                bool val[kChunk];
+#pragma unroll
+                for (int j = 0; j < kChunk; ++j) {
+                    const int t = t0 + j;
+                    val[j] = t < nsteps;
+                    const int mu = lam - t;
+                    const int row = cur + rl(off, (val[j] ? mu : lam) - lam_min);
+                    const int rrow = val[j] ? row : 0;
+                    kr[j] = ld16(Ks + (size_t)rrow * D + lane * 8);
+                    vr[j] = ld16(Vs + (size_t)rrow * D + lane * 8);
+                    cur = heap_parent(cur, p.bdiv);
+                }
+                float sc[kChunk];
+#pragma unroll
+                for (int j = 0; j < kChunk; ++j) {
+                    const float d = group_sum<LPR>(dot8<T>(qcur, kr[j])) * p.scale_log2;
+                    sc[j] = val[j] ? d : -INFINITY;
+                }
+                softmax_fold<T, kChunk>(m, l, acc, sc, vr);
+            }
+            write_out<T, LSE>(p, qrow, qh, lane, m, l, acc);
+        }
+        qcur = qnext;
+        lam = lam_n;
+        s0 = s0_n;
+        items = items_n;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Ancestor table kernel (debug export of the walk)
+// ---------------------------------------------------------------------------
+template <int WALK>
+__global__ __launch_bounds__(kThreads) void ancestors_kernel(TreeParams p, int32_t* out) {
+    const int64_t idx = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    const int seq = (int)(idx / p.max_seqlen);
+    const int tok = (int)(idx % p.max_seqlen);
+    if (seq >= p.B) return;
+    int32_t start, n;
+    if (!seq_bounds(p, seq, start, n)) return;
+    if (tok >= n) return;
+    int32_t* row = out + ((int64_t)start + tok) * (p.max_depth + 1);
+    int32_t cur = tok, prev = -1;
+    for (int s = 0; s <= p.max_depth; ++s) {
+        row[s] = (cur != prev) ? cur : -1;
+        prev = cur;
+        cur = walk_next<WALK>(p, start, n, cur);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// LSE merge kernel
+// ---------------------------------------------------------------------------
+struct MergeParams {
+    const float* lse_p;
+    const float* lse_t;
+    const void* o_p;
+    const void* o_t;
+    void* out;
+    int64_t sl_p[3], sl_t[3], so_p[4], so_t[4], so[4];
+    int32_t B, H, Nq;
+};
+
+template <typename T, int D>
+__global__ __launch_bounds__(kThreads) void lse_merge_kernel(MergeParams mp) {
+    constexpr int LPR = D / 8;
+    constexpr int SLOTS = kThreads / LPR;
+    const int lane = threadIdx.x % LPR;
+    const int64_t pos = (int64_t)blockIdx.x * SLOTS + threadIdx.x / LPR;
+    if (pos >= (int64_t)mp.B * mp.H * mp.Nq) return;
+    const int i = (int)(pos % mp.Nq);
+    const int h = (int)((pos / mp.Nq) % mp.H);
+    const int bb = (int)(pos / ((int64_t)mp.Nq * mp.H));
+    const float lp = mp.lse_p[bb * mp.sl_p[0] + h * mp.sl_p[1] + i * mp.sl_p[2]];
+    const float lt = mp.lse_t[bb * mp.sl_t[0] + h * mp.sl_t[1] + i * mp.sl_t[2]];
+    const float mx = fmaxf(lp, lt);
+    const float wp = fast_exp2((lp - mx) * kLog2e);
+    const float wt = fast_exp2((lt - mx) * kLog2e);
+    const float ws = fmaxf(wp + wt, 1e-8f);
+    const Vec16 a = ld16((const uint16_t*)mp.o_p + bb * mp.so_p[0] + h * mp.so_p[1] + i * mp.so_p[2] + lane * 8);
+    const Vec16 c = ld16((const uint16_t*)mp.o_t + bb * mp.so_t[0] + h * mp.so_t[1] + i * mp.so_t[2] + lane * 8);
+    float r[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) r[j] = (wp * elem<T>(a, j) + wt * elem<T>(c, j)) / ws;
+    st16((uint16_t*)mp.out + bb * mp.so[0] + h * mp.so[1] + i * mp.so[2] + lane * 8, pack8<T>(r));
+}
+
+// ---------------------------------------------------------------------------
+// Host side: validation, planning, dispatch
+// ---------------------------------------------------------------------------
+static bool row_aligned(const void* ptr, const int64_t* st, int n_outer) {
+    if (((uintptr_t)ptr & 15u) != 0) return false;
+    for (int i = 0; i < n_outer; ++i)
+        if (st[i] % 8 != 0) return false;
+    return st[n_outer] == 1;
+}
+
+static int check_common(int32_t dtype, int32_t head_dim, int32_t batch, int32_t max_seqlen,
+                        int64_t total_tokens, int32_t hq, int32_t hkv, int32_t max_depth) {
+    if (dtype != QATTN_DTYPE_F16 && dtype != QATTN_DTYPE_BF16) {
+        set_error("dtype %d is not fp16 (0) or bf16 (1)", dtype);
+        return QATTN_ERR_DTYPE;
+    }
+    if (head_dim != 32 && head_dim != 64 && head_dim != 128) {
+        set_error("head_dim %d not in {32, 64, 128}", head_dim);
+        return QATTN_ERR_HEAD_DIM;
+    }
+    if (batch < 0 || max_seqlen < 0 || total_tokens < 0 || hq < 1 || hkv < 1 || hq % hkv != 0 ||
+        max_depth < 0) {
+        set_error("bad sizes: batch=%d max_seqlen=%d total_tokens=%lld hq=%d hkv=%d max_depth=%d", batch,
+                  max_seqlen, (long long)total_tokens, hq, hkv, max_depth);
+        return QATTN_ERR_ARG;
+    }
+    if (total_tokens >= (int64_t(1) << 31) || (int64_t)max_seqlen * batch >= (int64_t(1) << 40)) {
+        set_error("sizes too large: total_tokens=%lld", (long long)total_tokens);
+        return QATTN_ERR_ARG;
+    }
+    return QATTN_OK;
+}
+
+static int launch_status(const char* what) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        set_error("%s: %s", what, hipGetErrorString(e));
+        return QATTN_ERR_HIP;
+    }
+    return QATTN_OK;
+}
+
+// Subtree tiling plan for a heap tree of n nodes (see DESIGN.md for the
+// derivation).  Returns false when no plan fits the LDS budget.
+static bool make_subtree_plan(int b, int64_t n, int max_depth, int rcap, SubtreePlan& plan) {
+    plan = SubtreePlan{};
+    if (n <= 0 || b < 1) return false;
+    if (b == 1) {
+        const int extra = (int)std::min<int64_t>(max_depth, n - 1);
+        int h = rcap - extra;
+        h = std::min(h, 64 - extra);
+        if (h < 1) return false;
+        h = (int)std::min<int64_t>(h, n);
+        plan.nbands = 1;
+        plan.chain_h = h;
+        plan.band[0] = Band{0, (int32_t)(n - 1), 1, 0};
+        const int64_t tiles = (n + h - 1) / h;
+        if (tiles >= (int64_t(1) << 30)) return false;
+        plan.total_tiles = (int32_t)tiles;
+        plan.max_rows = h + extra;
+        return true;
+    }
+    // level starts s[l] and full widths w[l]
+    std::vector<int64_t> s, w;
+    int64_t sl = 0, wl = 1;
+    while (sl < n) {
+        s.push_back(sl);
+        w.push_back(wl);
+        sl += wl;
+        if (wl > n) wl = n + 1; else wl *= b;
+    }
+    const int Lmax = (int)s.size() - 1;
+    auto width = [&](int l) -> int64_t { return std::min<int64_t>(w[l], n - s[l]); };
+    auto subtree = [&](int h) -> int64_t {  // nodes of one complete root subtree, h levels
+        int64_t tot = 0, bj = 1;
+        for (int j = 0; j < h; ++j) {
+            tot += bj;
+            if (tot > rcap) return int64_t(rcap) + 1;
+            bj *= b;
+        }
+        return tot;
+    };
+    auto extra_rows = [&](int64_t G, int lo) -> int64_t {  // ancestors above G adjacent roots
+        int64_t tot = 0, bj = 1;
+        const int J = std::min(lo, max_depth);
+        for (int j = 1; j <= J; ++j) {
+            if (bj <= n) bj *= b;
+            const int64_t span = (G - 1 + bj - 1) / bj + 1;
+            tot += std::min<int64_t>(span, width(lo - j));
+        }
+        return tot;
+    };
+    std::vector<Band> bands;
+    int hi = Lmax;
+    while (hi >= 0) {
+        int best = 0;
+        for (int h = 1; h <= hi + 1; ++h) {
+            const int lo = hi - h + 1;
+            const int nlev = hi - std::max(0, lo - max_depth) + 1;
+            if (subtree(h) + extra_rows(1, lo) > rcap || nlev > 64) break;
+            best = h;
+        }
+        if (best == 0) return false;
+        const int lo = hi - best + 1;
+        const int64_t size = subtree(best);
+        const int64_t wlo = width(lo);
+        int64_t G = 1;
+        while (G < wlo && (G + 1) * size + extra_rows(G + 1, lo) <= rcap) ++G;
+        bands.push_back(Band{lo, hi, (int32_t)G, 0});
+        if ((int)bands.size() > kMaxBands) return false;
+        hi = lo - 1;
+    }
+    std::reverse(bands.begin(), bands.end());  // top band first
+    int64_t tiles = 0, rows = 0;
+    for (size_t i = 0; i < bands.size(); ++i) {
+        Band& bd = bands[i];
+        bd.tile_base = (int32_t)tiles;
+        const int64_t wlo = width(bd.lo);
+        tiles += (wlo + bd.G - 1) / bd.G;
+        rows = std::max<int64_t>(rows, bd.G * subtree(bd.hi - bd.lo + 1) + extra_rows(bd.G, bd.lo));
+        plan.band[i] = bd;
+    }
+    if (tiles >= (int64_t(1) << 30)) return false;
+    plan.nbands = (int32_t)bands.size();
+    plan.total_tiles = (int32_t)tiles;
+    plan.max_rows = (int32_t)rows;
+    plan.chain_h = 0;
+    return rows <= rcap;
+}
+
+template <typename T, int D, int WALK, int LAYOUT, bool LSE, bool PSTATE>
+static int launch_gather(const TreeParams& p, hipStream_t st) {
+    constexpr int SLOTS = kThreads / (D / 8);
+    const int64_t slots = (int64_t)p.B * p.max_seqlen * p.Hq;
+    const int64_t blocks = (slots + SLOTS - 1) / SLOTS;
+    if (blocks >= (int64_t(1) << 31)) {
+        set_error("grid too large (%lld blocks)", (long long)blocks);
+        return QATTN_ERR_ARG;
+    }
+    hipLaunchKernelGGL((tree_gather_kernel<T, D, WALK, LAYOUT, LSE, PSTATE>), dim3((unsigned)blocks),
+                       dim3(kThreads), 0, st, p);
+    return launch_status("tree_gather_kernel");
+}
+
+template <typename T, int D, bool LSE, bool PSTATE>
+static int launch_subtree(const TreeParams& p, const SubtreePlan& plan, hipStream_t st) {
+    const int64_t blocks = (int64_t)p.B * p.Hkv * plan.total_tiles;
+    if (blocks >= (int64_t(1) << 31)) {
+        set_error("grid too large (%lld blocks)", (long long)blocks);
+        return QATTN_ERR_ARG;
+    }
+    const size_t lds = (size_t)plan.max_rows * D * 2 * sizeof(uint16_t);
+    hipLaunchKernelGGL((tree_subtree_kernel<T, D, LSE, PSTATE>), dim3((unsigned)blocks), dim3(kThreads), lds, st, p,
+                       plan, make_divider(p.group));
+    return launch_status("tree_subtree_kernel");
+}
+
+template <typename T, int D>
+static int dispatch_tree(const TreeParams& p, int walk, int layout, bool lse, bool pstate, int algo,
+                         hipStream_t st) {
+    if (walk == WALK_HEAP && layout == KV_PACKED && algo != QATTN_ALGO_GATHER) {
+        SubtreePlan plan;
+        const int rcap = kLdsBudget / (4 * D);
+        const bool ok = make_subtree_plan(p.bdiv.d, p.max_seqlen, p.max_depth, rcap, plan);
+        const int64_t wgs = ok ? (int64_t)p.B * p.Hkv * plan.total_tiles : 0;
+        // The subtree kernel needs enough tiles to fill 256 CUs; a merged
+        // prefix state makes each query heavier, so it only pays off there
+        // when tiles are plentiful.
+        const bool use = ok && (algo == QATTN_ALGO_SUBTREE || wgs >= (pstate ? 2048 : 512));
+        if (algo == QATTN_ALGO_SUBTREE && !ok) {
+            set_error("no subtree plan fits (b=%d, max_seqlen=%d, max_depth=%d)", p.bdiv.d, p.max_seqlen,
+                      p.max_depth);
+            return QATTN_ERR_ARG;
+        }
+        if (use) {
+            if (lse) {
+                return pstate ? launch_subtree<T, D, true, true>(p, plan, st)
+                              : launch_subtree<T, D, true, false>(p, plan, st);
+            }
+            return pstate ? launch_subtree<T, D, false, true>(p, plan, st)
+                          : launch_subtree<T, D, false, false>(p, plan, st);
+        }
+    } else if (algo == QATTN_ALGO_SUBTREE) {
+        set_error("the subtree kernel supports the heap walk on packed K/V only");
+        return QATTN_ERR_ARG;
+    }
+    if (walk == WALK_HEAP && layout == KV_PACKED) {
+        if (pstate) {
+            return lse ? launch_gather<T, D, WALK_HEAP, KV_PACKED, true, true>(p, st)
+                       : launch_gather<T, D, WALK_HEAP, KV_PACKED, false, true>(p, st);
+        }
+        return lse ? launch_gather<T, D, WALK_HEAP, KV_PACKED, true, false>(p, st)
+                   : launch_gather<T, D, WALK_HEAP, KV_PACKED, false, false>(p, st);
+    }
+    if (walk == WALK_PARENTS) {
+        return lse ? launch_gather<T, D, WALK_PARENTS, KV_PACKED, true, false>(p, st)
+                   : launch_gather<T, D, WALK_PARENTS, KV_PACKED, false, false>(p, st);
+    }
+    return lse ? launch_gather<T, D, WALK_HEAP, KV_PAGED, true, false>(p, st)
+               : launch_gather<T, D, WALK_HEAP, KV_PAGED, false, false>(p, st);
+}
+
+int run_tree(const TreeParams& p, int dtype, int head_dim, int walk, int layout, bool pstate, int algo,
+             hipStream_t st) {
+    const bool lse = p.lse != nullptr;
+    if (dtype == QATTN_DTYPE_F16) {
+        switch (head_dim) {
+            case 32: return dispatch_tree<F16, 32>(p, walk, layout, lse, pstate, algo, st);
+            case 64: return dispatch_tree<F16, 64>(p, walk, layout, lse, pstate, algo, st);
+            default: return dispatch_tree<F16, 128>(p, walk, layout, lse, pstate, algo, st);
+        }
+    }
+    switch (head_dim) {
+        case 32: return dispatch_tree<BF16, 32>(p, walk, layout, lse, pstate, algo, st);
+        case 64: return dispatch_tree<BF16, 64>(p, walk, layout, lse, pstate, algo, st);
+        default: return dispatch_tree<BF16, 128>(p, walk, layout, lse, pstate, algo, st);
+    }
+}
+
+// Fill the fields shared by the tree entry points.  Returns an error code.
+int fill_tree_params(TreeParams& p, const void* q, const int64_t* qs, const void* k, const int64_t* ks,
+                     const void* v, const int64_t* vs, void* o, const int64_t* os, float* lse,
+                     const int64_t* lss, const int32_t* cu, int32_t batch, int32_t max_seqlen,
+                     int64_t total_tokens, int32_t hq, int32_t hkv, int32_t b, int32_t max_depth, float scale) {
+    p = TreeParams{};
+    if (!q || !qs || !k || !ks || !v || !vs || !o || !os || !cu || (lse && !lss)) {
+        set_error("null pointer argument");
+        return QATTN_ERR_ARG;
+    }
+    if (b < 1) {
+        set_error("branching_factor %d < 1", b);
+        return QATTN_ERR_ARG;
+    }
+    if (!row_aligned(q, qs, 2) || !row_aligned(o, os, 2)) {
+        set_error("q/o rows must be 16-byte aligned with stride_dim 1");
+        return QATTN_ERR_LAYOUT;
+    }
+    if (!(scale == scale)) {
+        set_error("scale is NaN");
+        return QATTN_ERR_ARG;
+    }
+    p.q = q;
+    p.k = k;
+    p.v = v;
+    p.o = o;
+    p.lse = lse;
+    p.cu = cu;
+    p.sq_t = qs[0];
+    p.sq_h = qs[1];
+    p.sk_t = ks[0];
+    p.sk_h = ks[1];
+    p.sv_t = vs[0];
+    p.sv_h = vs[1];
+    p.so_t = os[0];
+    p.so_h = os[1];
+    if (lse) {
+        p.slse_t = lss[0];
+        p.slse_h = lss[1];
+    }
+    p.total_tokens = total_tokens;
+    p.kv_rows = total_tokens;
+    p.B = batch;
+    p.Hq = hq;
+    p.Hkv = hkv;
+    p.group = hq / hkv;
+    p.max_seqlen = max_seqlen;
+    p.max_depth = max_depth;
+    p.bdiv = make_divider(b);
+    p.scale_log2 = scale * kLog2e;
+    return QATTN_OK;
+}
+
+}  // namespace qattn
+
+using namespace qattn;
+
+extern "C" {
+
+const char* qattn_version(void) { return "qattention_amd 0.1.0 (gfx950)"; }
+
+const char* qattn_last_error(void) { return g_err; }
+
+int qattn_tree_fwd(const void* q, const int64_t q_stride[3], const void* k, const int64_t k_stride[3],
+                   const void* v, const int64_t v_stride[3], void* o, const int64_t o_stride[3], float* lse,
+                   const int64_t lse_stride[2], const int32_t* cu_seqlens, int32_t batch, int32_t max_seqlen,
+                   int64_t total_tokens, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                   int32_t branching_factor, int32_t max_depth, float scale, int32_t dtype, int32_t algo,
+                   void* stream) {
+    g_err[0] = 0;
+    int rc = check_common(dtype, head_dim, batch, max_seqlen, total_tokens, num_q_heads, num_kv_heads, max_depth);
+    if (rc) return rc;
+    TreeParams p;
+    rc = fill_tree_params(p, q, q_stride, k, k_stride, v, v_stride, o, o_stride, lse, lse_stride, cu_seqlens,
+                          batch, max_seqlen, total_tokens, num_q_heads, num_kv_heads, branching_factor, max_depth,
+                          scale);
+    if (rc) return rc;
+    if (!row_aligned(k, k_stride, 2) || !row_aligned(v, v_stride, 2)) {
+        set_error("k/v rows must be 16-byte aligned with stride_dim 1");
+        return QATTN_ERR_LAYOUT;
+    }
+    if (algo < QATTN_ALGO_AUTO || algo > QATTN_ALGO_SUBTREE) {
+        set_error("unknown algo %d", algo);
+        return QATTN_ERR_ARG;
+    }
+    if (batch == 0 || max_seqlen == 0 || total_tokens == 0) return QATTN_OK;
+    return run_tree(p, dtype, head_dim, WALK_HEAP, KV_PACKED, false, algo, (hipStream_t)stream);
+}
+
+int qattn_tree_parents_fwd(const void* q, const int64_t q_stride[3], const void* k, const int64_t k_stride[3],
+                           const void* v, const int64_t v_stride[3], void* o, const int64_t o_stride[3],
+                           float* lse, const int64_t lse_stride[2], const int32_t* cu_seqlens,
+                           const int32_t* parents, int32_t batch, int32_t max_seqlen, int64_t total_tokens,
+                           int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, int32_t max_depth,
+                           float scale, int32_t dtype, void* stream) {
+    g_err[0] = 0;
+    int rc = check_common(dtype, head_dim, batch, max_seqlen, total_tokens, num_q_heads, num_kv_heads, max_depth);
+    if (rc) return rc;
+    if (!parents) {
+        set_error("parents is null");
+        return QATTN_ERR_ARG;
+    }
+    TreeParams p;
+    rc = fill_tree_params(p, q, q_stride, k, k_stride, v, v_stride, o, o_stride, lse, lse_stride, cu_seqlens,
+                          batch, max_seqlen, total_tokens, num_q_heads, num_kv_heads, 1, max_depth, scale);
+    if (rc) return rc;
+    if (!row_aligned(k, k_stride, 2) || !row_aligned(v, v_stride, 2)) {
+        set_error("k/v rows must be 16-byte aligned with stride_dim 1");
+        return QATTN_ERR_LAYOUT;
+    }
+    p.parents = parents;
+    if (batch == 0 || max_seqlen == 0 || total_tokens == 0) return QATTN_OK;
+    return run_tree(p, dtype, head_dim, WALK_PARENTS, KV_PACKED, false, QATTN_ALGO_GATHER, (hipStream_t)stream);
+}
+
+int qattn_tree_paged_fwd(const void* q, const int64_t q_stride[3], const void* k_cache, const int64_t k_stride[4],
+                         const void* v_cache, const int64_t v_stride[4], void* o, const int64_t o_stride[3],
+                         float* lse, const int64_t lse_stride[2], const int32_t* cu_seqlens,
+                         const int32_t* page_table, int32_t pt_cols, int32_t num_pages, int32_t page_size,
+                         int32_t batch, int32_t max_seqlen, int64_t total_tokens, int32_t num_q_heads,
+                         int32_t num_kv_heads, int32_t head_dim, int32_t branching_factor, int32_t max_depth,
+                         float scale, int32_t dtype, void* stream) {
+    g_err[0] = 0;
+    int rc = check_common(dtype, head_dim, batch, max_seqlen, total_tokens, num_q_heads, num_kv_heads, max_depth);
+    if (rc) return rc;
+    if (!page_table || !k_stride || !v_stride || page_size < 1 || pt_cols < 0 || num_pages < 0) {
+        set_error("bad paged arguments: page_size=%d pt_cols=%d num_pages=%d", page_size, pt_cols, num_pages);
+        return QATTN_ERR_ARG;
+    }
+    // The walk's K/V access is page * stride_page + slot * stride_slot + head * stride_head.
+    const int64_t ks3[3] = {k_stride[1], k_stride[2], k_stride[3]};
+    const int64_t vs3[3] = {v_stride[1], v_stride[2], v_stride[3]};
+    TreeParams p;
+    rc = fill_tree_params(p, q, q_stride, k_cache, ks3, v_cache, vs3, o, o_stride, lse, lse_stride, cu_seqlens,
+                          batch, max_seqlen, total_tokens, num_q_heads, num_kv_heads, branching_factor, max_depth,
+                          scale);
+    if (rc) return rc;
+    if (!row_aligned(k_cache, ks3, 2) || !row_aligned(v_cache, vs3, 2) || k_stride[0] % 8 || v_stride[0] % 8) {
+        set_error("k/v cache rows must be 16-byte aligned with stride_dim 1");
+        return QATTN_ERR_LAYOUT;
+    }
+    p.page_table = page_table;
+    p.pt_cols = pt_cols;
+    p.num_pages = num_pages;
+    p.page_size = page_size;
+    p.sk_page = k_stride[0];
+    p.sv_page = v_stride[0];
+    if (batch == 0 || max_seqlen == 0 || total_tokens == 0) return QATTN_OK;
+    return run_tree(p, dtype, head_dim, WALK_HEAP, KV_PAGED, false, QATTN_ALGO_GATHER, (hipStream_t)stream);
+}
+
+int qattn_ancestors(const int32_t* cu_seqlens, const int32_t* parents, int32_t batch, int32_t max_seqlen,
+                    int64_t total_tokens, int32_t branching_factor, int32_t max_depth, int32_t* out,
+                    void* stream) {
+    g_err[0] = 0;
+    if (!cu_seqlens || !out || batch < 0 || max_seqlen < 0 || total_tokens < 0 || max_depth < 0 ||
+        (!parents && branching_factor < 1) || total_tokens >= (int64_t(1) << 31)) {
+        set_error("bad arguments to qattn_ancestors");
+        return QATTN_ERR_ARG;
+    }
+    if (batch == 0 || max_seqlen == 0 || total_tokens == 0) return QATTN_OK;
+    TreeParams p{};
+    p.cu = cu_seqlens;
+    p.parents = parents;
+    p.B = batch;
+    p.max_seqlen = max_seqlen;
+    p.total_tokens = total_tokens;
+    p.max_depth = max_depth;
+    p.bdiv = make_divider(parents ? 1 : branching_factor);
+    const int64_t n = (int64_t)batch * max_seqlen;
+    const int64_t blocks = (n + kThreads - 1) / kThreads;
+    if (parents)
+        hipLaunchKernelGGL(ancestors_kernel<WALK_PARENTS>, dim3((unsigned)blocks), dim3(kThreads), 0,
+                           (hipStream_t)stream, p, out);
+    else
+        hipLaunchKernelGGL(ancestors_kernel<WALK_HEAP>, dim3((unsigned)blocks), dim3(kThreads), 0,
+                           (hipStream_t)stream, p, out);
+    return launch_status("ancestors_kernel");
+}
+
+int qattn_lse_merge(const float* lse_pre, const int64_t lse_pre_stride[3], const float* lse_tree,
+                    const int64_t lse_tree_stride[3], const void* o_pre, const int64_t o_pre_stride[4],
+                    const void* o_tree, const int64_t o_tree_stride[4], void* out, const int64_t out_stride[4],
+                    int32_t B, int32_t H, int32_t Nq, int32_t head_dim, int32_t dtype, void* stream) {
+    g_err[0] = 0;
+    if (!lse_pre || !lse_tree || !o_pre || !o_tree || !out || !lse_pre_stride || !lse_tree_stride ||
+        !o_pre_stride || !o_tree_stride || !out_stride || B < 0 || H < 0 || Nq < 0) {
+        set_error("bad arguments to qattn_lse_merge");
+        return QATTN_ERR_ARG;
+    }
+    if (dtype != QATTN_DTYPE_F16 && dtype != QATTN_DTYPE_BF16) {
+        set_error("dtype %d is not fp16 (0) or bf16 (1)", dtype);
+        return QATTN_ERR_DTYPE;
+    }
+    if (head_dim != 32 && head_dim != 64 && head_dim != 128) {
+        set_error("head_dim %d not in {32, 64, 128}", head_dim);
+        return QATTN_ERR_HEAD_DIM;
+    }
+    if (!row_aligned(o_pre, o_pre_stride, 3) || !row_aligned(o_tree, o_tree_stride, 3) ||
+        !row_aligned(out, out_stride, 3)) {
+        set_error("merge operands must have stride_dim 1 and 16-byte aligned rows");
+        return QATTN_ERR_LAYOUT;
+    }
+    const int64_t npos = (int64_t)B * H * Nq;
+    if (npos == 0) return QATTN_OK;
+    MergeParams mp{};
+    mp.lse_p = lse_pre;
+    mp.lse_t = lse_tree;
+    mp.o_p = o_pre;
+    mp.o_t = o_tree;
+    mp.out = out;
+    for (int i = 0; i < 3; ++i) {
+        mp.sl_p[i] = lse_pre_stride[i];
+        mp.sl_t[i] = lse_tree_stride[i];
+    }
+    for (int i = 0; i < 4; ++i) {
+        mp.so_p[i] = o_pre_stride[i];
+        mp.so_t[i] = o_tree_stride[i];
+        mp.so[i] = out_stride[i];
+    }
+    mp.B = B;
+    mp.H = H;
+    mp.Nq = Nq;
+    const int slots = kThreads / (head_dim / 8);
+    const int64_t blocks = (npos + slots - 1) / slots;
+    if (blocks >= (int64_t(1) << 31)) {
+        set_error("grid too large");
+        return QATTN_ERR_ARG;
+    }
+    hipStream_t st = (hipStream_t)stream;
+#define QATTN_MERGE(T, D) \
+    hipLaunchKernelGGL((lse_merge_kernel<T, D>), dim3((unsigned)blocks), dim3(kThreads), 0, st, mp)
+    if (dtype == QATTN_DTYPE_F16) {
+        if (head_dim == 32) QATTN_MERGE(F16, 32);
+        else if (head_dim == 64) QATTN_MERGE(F16, 64);
+        else QATTN_MERGE(F16, 128);
+    } else {
+        if (head_dim == 32) QATTN_MERGE(BF16, 32);
+        else if (head_dim == 64) QATTN_MERGE(BF16, 64);
+        else QATTN_MERGE(BF16, 128);
+    }
+#undef QATTN_MERGE
+    return launch_status("lse_merge_kernel");
+}
+
+}  // extern "C"

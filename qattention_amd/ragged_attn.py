@@ -1,0 +1,382 @@
+"""Ancestor-sparse tree-verify attention on MI355X -- the `src.ragged_attn` API.
+
+Host side of the drop-in replacement for the reference module
+src/ragged_attn.py (saifmb0/QAttention).  Names, argument order, defaults,
+return values and error behaviour follow the reference; the work is done by
+hand-written gfx950 HIP kernels in libqattn.so, called through its C ABI
+(include/qattn.h) on torch's current HIP stream.  Outputs are allocated here
+through the torch caching allocator, so a call allocates nothing inside the
+library and is HIP-graph capturable when max_seqlen is given (no host sync).
+
+Differences from the reference, all supersets:
+  * K/V may carry fewer heads than Q (GQA): q head h reads kv head
+    h // (Hq // Hkv), exactly what repeat_kv would have produced.
+  * Inputs whose last dim is not unit-stride or whose rows are not 16-byte
+    aligned are copied to a contiguous layout first (the reference accepts any
+    strides; the HIP kernels read 16-byte vectors).
+  * bf16 runs natively (the reference casts bf16 to fp16 below SM 8.9,
+    src/ragged_attn.py:1118-1127; gfx950 has bf16 dot/MFMA instructions).
+"""
+from __future__ import annotations
+
+import math
+from typing import List, Optional, Tuple
+
+import torch
+
+from . import _lib
+
+_SUPPORTED = (torch.float16, torch.bfloat16)
+
+
+# ---------------------------------------------------------------------------
+# helpers
+# ---------------------------------------------------------------------------
+
+def _check_dtypes(Q, K, V):
+    # src/ragged_attn.py:1113-1116
+    assert Q.dtype in _SUPPORTED and Q.dtype == K.dtype == V.dtype, (
+        f"Inputs must be fp16 or bf16 (got {Q.dtype})"
+    )
+
+
+def _dtype_code(t: torch.Tensor) -> int:
+    return _lib.DTYPE_F16 if t.dtype == torch.float16 else _lib.DTYPE_BF16
+
+
+def _vec_ok(t: torch.Tensor) -> bool:
+    """Rows readable as 16-byte vectors: unit last stride, 8-element aligned
+    outer strides, 16-byte aligned base."""
+    if t.numel() == 0:
+        return True
+    st = t.stride()
+    return st[-1] == 1 and all(s % 8 == 0 for s in st[:-1]) and t.data_ptr() % 16 == 0
+
+
+def _vec(t: torch.Tensor) -> torch.Tensor:
+    return t if _vec_ok(t) else t.contiguous()
+
+
+def _require_device(*ts):
+    dev = ts[0].device
+    if dev.type != "cuda":
+        raise RuntimeError(
+            "qattention_amd runs on a ROCm GPU only (got tensors on "
+            f"{dev}); there is no CPU path")
+    for t in ts[1:]:
+        if t.device != dev:
+            raise RuntimeError(f"all tensors must be on {dev} (got {t.device})")
+    return dev
+
+
+def _stream(device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _seqlens(cu_seqlens: torch.Tensor, B: int, device, max_seqlen: Optional[int]):
+    """max_seqlen and a device int32 copy of cu_seqlens (src/ragged_attn.py:1136-1142).
+
+    When max_seqlen is None it is computed from a host copy of cu_seqlens
+    (a device->host sync only if cu_seqlens lives on the GPU, as in the
+    reference); pass it explicitly for graph capture."""
+    if max_seqlen is None:
+        cu_cpu = cu_seqlens.cpu()
+        sl = cu_cpu.tolist()
+        max_seqlen = int(max(sl[i + 1] - sl[i] for i in range(B))) if B else 1
+        cu_dev = cu_cpu.to(device=device, dtype=torch.int32, non_blocking=True)
+    else:
+        cu_dev = cu_seqlens.to(device=device, dtype=torch.int32, non_blocking=True)
+    return max(int(max_seqlen), 0), cu_dev.contiguous()
+
+
+def _heads(Q, K, V):
+    T, Hq, D = Q.shape
+    Hkv = K.shape[1]
+    if K.shape[-1] != D or V.shape[-1] != D or V.shape[-2] != Hkv:
+        raise ValueError(f"shape mismatch: Q {tuple(Q.shape)} K {tuple(K.shape)} V {tuple(V.shape)}")
+    if Hkv < 1 or Hq % Hkv != 0:
+        raise ValueError(f"num q heads {Hq} must be a multiple of num kv heads {Hkv}")
+    return T, Hq, Hkv, D
+
+
+# ---------------------------------------------------------------------------
+# core launcher for the heap walk
+# ---------------------------------------------------------------------------
+
+def _tree_forward(Q, K, V, cu_seqlens, branching_factor: int, max_depth: int,
+                  max_seqlen: Optional[int], want_lse: bool, algo: int = _lib.ALGO_AUTO):
+    _check_dtypes(Q, K, V)
+    device = _require_device(Q, K, V)
+    T, Hq, Hkv, D = _heads(Q, K, V)
+    if K.shape[0] != T or V.shape[0] != T:
+        raise ValueError("packed Q, K, V must have the same number of tokens")
+    B = int(cu_seqlens.shape[0]) - 1
+    ms, cu_dev = _seqlens(cu_seqlens, B, device, max_seqlen)
+    Q, K, V = _vec(Q), _vec(K), _vec(V)
+    O = torch.empty_like(Q)
+    if not _vec_ok(O):
+        O = torch.empty(Q.shape, dtype=Q.dtype, device=device)
+    LSE = torch.empty(T, Hq, dtype=torch.float32, device=device) if want_lse else None
+    scale = 1.0 / math.sqrt(D)
+    L = _lib.lib()
+    with torch.cuda.device(device):
+        rc = L.qattn_tree_fwd(
+            Q.data_ptr(), _lib.i64arr(Q.stride()), K.data_ptr(), _lib.i64arr(K.stride()),
+            V.data_ptr(), _lib.i64arr(V.stride()), O.data_ptr(), _lib.i64arr(O.stride()),
+            _lib.ptr(LSE), _lib.i64arr(LSE.stride()) if LSE is not None else None,
+            cu_dev.data_ptr(), B, ms, T, Hq, Hkv, D, int(branching_factor), int(max_depth),
+            scale, _dtype_code(Q), int(algo), _stream(device))
+    _lib.check(rc, "qattn_tree_fwd")
+    return O, LSE
+
+
+# ---------------------------------------------------------------------------
+# public API (src/ragged_attn.py:1054-1166, 499-572, 1423-1556)
+# ---------------------------------------------------------------------------
+
+def pack_inputs(
+    qs: List[torch.Tensor],
+    ks: List[torch.Tensor],
+    vs: List[torch.Tensor],
+) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Concatenate per-sequence [L_i, H, D] tensors into the packed ragged
+    layout; cu_seqlens is a CPU int32 [B+1] prefix sum (src/ragged_attn.py:1054-1077)."""
+    assert len(qs) == len(ks) == len(vs)
+    lens = torch.tensor([0] + [q.shape[0] for q in qs], dtype=torch.int64)
+    cu_seqlens = torch.cumsum(lens, 0).to(torch.int32)
+    return torch.cat(qs, 0), torch.cat(ks, 0), torch.cat(vs, 0), cu_seqlens
+
+
+def ragged_attention(
+    Q: torch.Tensor,
+    K: torch.Tensor,
+    V: torch.Tensor,
+    cu_seqlens: torch.Tensor,
+    branching_factor: int,
+    max_depth: int,
+    max_seqlen: int = None,
+) -> torch.Tensor:
+    """Ancestor-sparse attention for BFS-ordered complete b-ary trees.
+
+    Query token x of each sequence attends to {parent^s(x) : s = 0..max_depth}
+    with parent(k) = max(k - 1, 0) // b (src/ragged_attn.py:1080-1166).
+    Q, K, V: packed [sum L_i, H, D] fp16/bf16 on the GPU (K/V may have fewer
+    heads, GQA); cu_seqlens: [B+1] int32 on host or device.
+    Returns O with Q's dtype and shape.
+    """
+    return _tree_forward(Q, K, V, cu_seqlens, branching_factor, max_depth, max_seqlen, False)[0]
+
+
+def ragged_attention_with_lse(
+    Q: torch.Tensor,
+    K: torch.Tensor,
+    V: torch.Tensor,
+    cu_seqlens: torch.Tensor,
+    branching_factor: int,
+    max_depth: int,
+    max_seqlen: int = None,
+) -> tuple:
+    """As ragged_attention, also returning LSE [sum L_i, H] fp32 (natural log)
+    for merging with another attention block (src/ragged_attn.py:499-572)."""
+    return _tree_forward(Q, K, V, cu_seqlens, branching_factor, max_depth, max_seqlen, True)
+
+
+def ragged_attention_sibling(
+    Q: torch.Tensor,
+    K: torch.Tensor,
+    V: torch.Tensor,
+    cu_seqlens: torch.Tensor,
+    branching_factor: int,
+    max_depth: int,
+    max_seqlen: int = None,
+) -> torch.Tensor:
+    """Same function as ragged_attention (src/ragged_attn.py:1423-1492).
+
+    The reference keeps a second Triton kernel that only reorders load issue;
+    here both names run the same HIP kernels, which already issue every
+    ancestor load of a step chunk before the softmax chain."""
+    return _tree_forward(Q, K, V, cu_seqlens, branching_factor, max_depth, max_seqlen, False)[0]
+
+
+def ragged_attention_sibling_with_lse(
+    Q: torch.Tensor,
+    K: torch.Tensor,
+    V: torch.Tensor,
+    cu_seqlens: torch.Tensor,
+    branching_factor: int,
+    max_depth: int,
+    max_seqlen: int = None,
+) -> tuple:
+    """Same function as ragged_attention_with_lse (src/ragged_attn.py:1495-1556)."""
+    return _tree_forward(Q, K, V, cu_seqlens, branching_factor, max_depth, max_seqlen, True)
+
+
+def ragged_attention_with_parents(
+    Q: torch.Tensor,
+    K: torch.Tensor,
+    V: torch.Tensor,
+    cu_seqlens: torch.Tensor,
+    parents: torch.Tensor,
+    max_depth: int,
+    max_seqlen: int = None,
+) -> tuple:
+    """Ancestor-sparse attention over an explicit parent array
+    (src/ragged_attn.py:716-795).
+
+    parents: int32 [sum L_i], sequence-local parent of every token; a root
+    must self-loop (parents[root] == root).  Returns (O, LSE)."""
+    _check_dtypes(Q, K, V)
+    device = _require_device(Q, K, V)
+    T, Hq, Hkv, D = _heads(Q, K, V)
+    if K.shape[0] != T or V.shape[0] != T:
+        raise ValueError("packed Q, K, V must have the same number of tokens")
+    if parents.numel() < T:
+        raise ValueError(f"parents has {parents.numel()} entries for {T} tokens")
+    B = int(cu_seqlens.shape[0]) - 1
+    ms, cu_dev = _seqlens(cu_seqlens, B, device, max_seqlen)
+    par = parents.to(device=device, dtype=torch.int32, non_blocking=True).contiguous()
+    Q, K, V = _vec(Q), _vec(K), _vec(V)
+    O = torch.empty_like(Q)
+    if not _vec_ok(O):
+        O = torch.empty(Q.shape, dtype=Q.dtype, device=device)
+    LSE = torch.empty(T, Hq, dtype=torch.float32, device=device)
+    L = _lib.lib()
+    with torch.cuda.device(device):
+        rc = L.qattn_tree_parents_fwd(
+            Q.data_ptr(), _lib.i64arr(Q.stride()), K.data_ptr(), _lib.i64arr(K.stride()),
+            V.data_ptr(), _lib.i64arr(V.stride()), O.data_ptr(), _lib.i64arr(O.stride()),
+            LSE.data_ptr(), _lib.i64arr(LSE.stride()), cu_dev.data_ptr(), par.data_ptr(),
+            B, ms, T, Hq, Hkv, D, int(max_depth), 1.0 / math.sqrt(D), _dtype_code(Q),
+            _stream(device))
+    _lib.check(rc, "qattn_tree_parents_fwd")
+    return O, LSE
+
+
+def ragged_attention_paged(
+    Q: torch.Tensor,
+    K_cache: torch.Tensor,
+    V_cache: torch.Tensor,
+    page_table: torch.Tensor,
+    cu_seqlens: torch.Tensor,
+    branching_factor: int,
+    max_depth: int,
+) -> torch.Tensor:
+    """Ancestor-sparse attention reading K/V from a paged cache
+    (src/ragged_attn.py:932-1003).
+
+    K_cache/V_cache: [pages, PAGE_SIZE, Hkv, D]; page_table: [B, max_pages]
+    int32 logical->physical page map; ancestor position c of sequence b is
+    slot c % PAGE_SIZE of page page_table[b, c // PAGE_SIZE]."""
+    assert K_cache.shape == V_cache.shape, "K and V cache shapes must match"
+    _check_dtypes(Q, K_cache, V_cache)
+    device = _require_device(Q, K_cache, V_cache)
+    T, Hq, D = Q.shape
+    num_pages, page_size, Hkv, Dk = K_cache.shape
+    if Dk != D or Hkv < 1 or Hq % Hkv != 0:
+        raise ValueError(f"cache shape {tuple(K_cache.shape)} incompatible with Q {tuple(Q.shape)}")
+    B = int(cu_seqlens.shape[0]) - 1
+    ms, cu_dev = _seqlens(cu_seqlens, B, device, None)  # the reference always reads cu on host
+    pt = page_table.to(device=device, dtype=torch.int32, non_blocking=True).contiguous()
+    if pt.dim() != 2 or pt.shape[0] < B:
+        raise ValueError(f"page_table must be [B, max_pages] (got {tuple(page_table.shape)})")
+    Q, K_cache, V_cache = _vec(Q), _vec(K_cache), _vec(V_cache)
+    O = torch.empty_like(Q)
+    if not _vec_ok(O):
+        O = torch.empty(Q.shape, dtype=Q.dtype, device=device)
+    L = _lib.lib()
+    with torch.cuda.device(device):
+        rc = L.qattn_tree_paged_fwd(
+            Q.data_ptr(), _lib.i64arr(Q.stride()), K_cache.data_ptr(), _lib.i64arr(K_cache.stride()),
+            V_cache.data_ptr(), _lib.i64arr(V_cache.stride()), O.data_ptr(), _lib.i64arr(O.stride()),
+            None, None, cu_dev.data_ptr(), pt.data_ptr(), int(pt.stride(0)), num_pages, page_size,
+            B, ms, T, Hq, Hkv, D, int(branching_factor), int(max_depth), 1.0 / math.sqrt(D),
+            _dtype_code(Q), _stream(device))
+    _lib.check(rc, "qattn_tree_paged_fwd")
+    return O
+
+
+def build_paged_kv(
+    ks: List[torch.Tensor],
+    vs: List[torch.Tensor],
+    page_size: int = 16,
+) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Pack per-sequence [L_i, H, D] K/V into a paged cache
+    (src/ragged_attn.py:1006-1047): pages are assigned in sequence order,
+    unused slots are zero; page_table is a CPU int32 [B, max_pages] tensor."""
+    B = len(ks)
+    H, D = ks[0].shape[1], ks[0].shape[2]
+    device, dtype = ks[0].device, ks[0].dtype
+    pages = [(k.shape[0] + page_size - 1) // page_size for k in ks]
+    max_pages, total = max(pages), sum(pages)
+    K_cache = torch.zeros(total, page_size, H, D, device=device, dtype=dtype)
+    V_cache = torch.zeros(total, page_size, H, D, device=device, dtype=dtype)
+    page_table = torch.zeros(B, max_pages, dtype=torch.int32)
+    phys = 0
+    for b, (k, v) in enumerate(zip(ks, vs)):
+        n = k.shape[0]
+        full = n // page_size
+        if full:
+            K_cache[phys:phys + full] = k[:full * page_size].reshape(full, page_size, H, D)
+            V_cache[phys:phys + full] = v[:full * page_size].reshape(full, page_size, H, D)
+        if n % page_size:
+            r = n % page_size
+            K_cache[phys + full, :r] = k[full * page_size:]
+            V_cache[phys + full, :r] = v[full * page_size:]
+        page_table[b, :pages[b]] = torch.arange(phys, phys + pages[b], dtype=torch.int32)
+        phys += pages[b]
+    return K_cache, V_cache, page_table
+
+
+def fused_lse_merge(
+    lse_pre: torch.Tensor,
+    lse_tree: torch.Tensor,
+    out_pre: torch.Tensor,
+    out_tree: torch.Tensor,
+) -> torch.Tensor:
+    """Online-softmax merge of two attention blocks (src/ragged_attn.py:1619-1653).
+
+    lse_*: [B, H, Nq] (any float dtype; read as fp32), out_*: [B, H, Nq, D]
+    fp16/bf16 of any layout with a unit last stride.  Returns a contiguous
+    [B, H, Nq, D] tensor in out_pre's dtype."""
+    B, H, Nq, D = out_pre.shape
+    if out_tree.shape != out_pre.shape or lse_pre.shape != (B, H, Nq) or lse_tree.shape != (B, H, Nq):
+        raise ValueError("fused_lse_merge: shape mismatch")
+    device = _require_device(out_pre, out_tree, lse_pre, lse_tree)
+    if out_pre.dtype not in _SUPPORTED:
+        raise AssertionError(f"Inputs must be fp16 or bf16 (got {out_pre.dtype})")
+    out_tree = out_tree.to(out_pre.dtype)
+    lse_p = lse_pre.float()
+    lse_t = lse_tree.float()
+    op, ot = _vec(out_pre), _vec(out_tree)
+    result = torch.empty(B, H, Nq, D, dtype=out_pre.dtype, device=device)
+    L = _lib.lib()
+    with torch.cuda.device(device):
+        rc = L.qattn_lse_merge(
+            lse_p.data_ptr(), _lib.i64arr(lse_p.stride()), lse_t.data_ptr(), _lib.i64arr(lse_t.stride()),
+            op.data_ptr(), _lib.i64arr(op.stride()), ot.data_ptr(), _lib.i64arr(ot.stride()),
+            result.data_ptr(), _lib.i64arr(result.stride()), B, H, Nq, D, _dtype_code(op),
+            _stream(device))
+    _lib.check(rc, "qattn_lse_merge")
+    return result
+
+
+def ancestor_table(cu_seqlens: torch.Tensor, branching_factor: int, max_depth: int,
+                   parents: Optional[torch.Tensor] = None, max_seqlen: int = None,
+                   device=None) -> torch.Tensor:
+    """Ancestor index table [sum L_i, max_depth+1] int32 from the device walk
+    (entry -1 = step not attended).  Exposes the walk the attention kernels
+    use (src/ragged_attn.py:323-377, :650-698) for bit-exact checks."""
+    device = torch.device(device) if device is not None else torch.device("cuda")
+    B = int(cu_seqlens.shape[0]) - 1
+    T = int(cu_seqlens[-1])
+    ms, cu_dev = _seqlens(cu_seqlens, B, device, max_seqlen)
+    out = torch.full((T, max_depth + 1), -1, dtype=torch.int32, device=device)
+    par = None
+    if parents is not None:
+        par = parents.to(device=device, dtype=torch.int32).contiguous()
+    L = _lib.lib()
+    with torch.cuda.device(device):
+        rc = L.qattn_ancestors(cu_dev.data_ptr(), _lib.ptr(par), B, ms, T, int(branching_factor),
+                               int(max_depth), out.data_ptr(), _stream(device))
+    _lib.check(rc, "qattn_ancestors")
+    return out

@@ -1,0 +1,14 @@
+"""`src.ragged_attn` drop-in: re-exports qattention_amd.ragged_attn."""
+from qattention_amd.ragged_attn import *  # noqa: F401,F403
+from qattention_amd.ragged_attn import (  # noqa: F401
+    ancestor_table,
+    build_paged_kv,
+    fused_lse_merge,
+    pack_inputs,
+    ragged_attention,
+    ragged_attention_paged,
+    ragged_attention_sibling,
+    ragged_attention_sibling_with_lse,
+    ragged_attention_with_lse,
+    ragged_attention_with_parents,
+)

@@ -1,0 +1,181 @@
+"""Host-side checks that need no GPU: the C ABI library loads and exports every
+declared symbol, argument validation returns the documented error codes
+before touching the device, and the host utilities match the oracle."""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import re
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import ROOT, make_inputs, num_tree_nodes
+from oracle import clib, tree
+from qattention_amd import _lib
+from qattention_amd import ragged_attn as ra
+from qattention_amd import tree_mask as tm
+
+HEADER = os.path.join(ROOT, "include", "qattn.h")
+
+
+def _declared_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(qattn_\w+)\s*\(", text)))
+
+
+def test_header_declares_entry_points():
+    syms = _declared_symbols()
+    for s in ("qattn_tree_fwd", "qattn_tree_parents_fwd", "qattn_tree_paged_fwd",
+              "qattn_ancestors", "qattn_lse_merge", "qattn_last_error", "qattn_version"):
+        assert s in syms
+
+
+def test_library_exports_every_declared_symbol():
+    L = _lib.lib()
+    for s in _declared_symbols():
+        assert hasattr(L, s), s
+        assert s in _lib.SIGNATURES, f"{s} has no ctypes signature"
+    assert L.qattn_version().startswith(b"qattention_amd")
+
+
+def test_single_hip_runtime_mapped():
+    _lib.lib()
+    maps = open(f"/proc/{os.getpid()}/maps").read()
+    hip = {l.split()[-1] for l in maps.splitlines() if "libamdhip64" in l}
+    assert len(hip) == 1, hip
+
+
+def _divide(x, d):
+    """Python restatement of qattn::make_divider / divide (qattn_common.h)."""
+    l = 0
+    while (1 << l) < d:
+        l += 1
+    m = ((1 << 32) * ((1 << l) - d)) // d + 1
+    hi = (x * m) >> 32
+    return ((hi + x) & 0xFFFFFFFF) >> l
+
+
+def test_divider_exact():
+    rng = np.random.default_rng(0)
+    xs = list(range(0, 4097)) + [2**31 - 1, 2**31 - 2, 2**30, 2**24 + 1] + \
+        [int(v) for v in rng.integers(0, 2**31, 2000)]
+    for d in list(range(1, 70)) + [100, 127, 1000, 4096, 65535, 65537, 2**20 + 7, 2**30 + 1, 2**31 - 1]:
+        for x in xs:
+            assert _divide(x, d) == x // d, (x, d)
+
+
+# ---------------------------------------------------------------------------
+# C ABI argument validation (returns before any device call)
+# ---------------------------------------------------------------------------
+
+FAKE = 1 << 20  # a non-null, 16-byte aligned address that is never dereferenced
+
+
+def _tree_call(dtype=0, head_dim=64, q=FAKE, qs=(256, 64, 1), hq=4, hkv=4, b=2, md=3, batch=1):
+    L = _lib.lib()
+    st = _lib.i64arr(qs)
+    ok = _lib.i64arr((256, 64, 1))
+    return L.qattn_tree_fwd(q, st, FAKE, ok, FAKE, ok, FAKE, ok, None, None, FAKE, batch, 15, 15,
+                            hq, hkv, head_dim, b, md, 0.125, dtype, 0, None)
+
+
+def test_abi_validation_codes():
+    assert _tree_call(dtype=7) == -2
+    assert _tree_call(head_dim=96) == -3
+    assert _tree_call(q=0) == -1
+    assert _tree_call(qs=(256, 64, 2)) == -4
+    assert _tree_call(qs=(250, 64, 1)) == -4
+    assert _tree_call(q=FAKE + 2) == -4
+    assert _tree_call(hq=6, hkv=4) == -1
+    assert _tree_call(b=0) == -1
+    assert _tree_call(md=-1) == -1
+    assert "head_dim" in _lib.last_error() or _tree_call(head_dim=96) == -3
+    assert _tree_call(batch=0) == 0  # nothing to do: no launch
+
+
+def test_abi_validation_other_entry_points():
+    L = _lib.lib()
+    ok3 = _lib.i64arr((256, 64, 1))
+    ok4 = _lib.i64arr((4096, 256, 64, 1))
+    assert L.qattn_tree_parents_fwd(FAKE, ok3, FAKE, ok3, FAKE, ok3, FAKE, ok3, FAKE, _lib.i64arr((4, 1)),
+                                    FAKE, None, 1, 15, 15, 4, 4, 64, 3, 0.125, 0, None) == -1
+    assert L.qattn_tree_paged_fwd(FAKE, ok3, FAKE, ok4, FAKE, ok4, FAKE, ok3, None, None, FAKE, FAKE,
+                                  4, 4, 0, 1, 15, 15, 4, 4, 64, 2, 3, 0.125, 0, None) == -1
+    assert L.qattn_ancestors(FAKE, None, 1, 15, 15, 0, 3, FAKE, None) == -1
+    s3 = _lib.i64arr((60, 15, 1))
+    assert L.qattn_lse_merge(FAKE, s3, FAKE, s3, FAKE, ok4, FAKE, ok4, FAKE, ok4, 1, 4, 15, 48, 0, None) == -3
+    assert L.qattn_lse_merge(FAKE, s3, FAKE, s3, FAKE, ok4, FAKE, ok4, FAKE, ok4, 1, 4, 15, 64, 3, None) == -2
+
+
+# ---------------------------------------------------------------------------
+# Python API behaviour on the host
+# ---------------------------------------------------------------------------
+
+def test_dtype_assertion_matches_reference():
+    Q, K, V, cu = make_inputs([7], 4, 64, 1, torch.float32)
+    with pytest.raises(AssertionError):
+        ra.ragged_attention(Q, K, V, cu, 2, 2)
+    Q16 = Q.half()
+    with pytest.raises(AssertionError):
+        ra.ragged_attention(Q16, K.bfloat16(), V.half(), cu, 2, 2)
+
+
+def test_cpu_tensors_fail_loudly():
+    Q, K, V, cu = make_inputs([7], 4, 64, 1, torch.float16)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        ra.ragged_attention(Q, K, V, cu, 2, 2)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        ra.ragged_attention_with_parents(Q, K, V, cu, torch.zeros(7, dtype=torch.int32), 2)
+
+
+def test_pack_inputs():
+    qs = [torch.randn(n, 2, 8) for n in (3, 0, 5)]
+    Q, K, V, cu = ra.pack_inputs(qs, qs, qs)
+    assert cu.dtype == torch.int32 and cu.tolist() == [0, 3, 3, 8]
+    assert torch.equal(Q, torch.cat(qs, 0)) and Q.shape == (8, 2, 8)
+
+
+def test_build_paged_kv_roundtrip():
+    g = torch.Generator().manual_seed(3)
+    ks = [torch.randn(n, 2, 8, generator=g) for n in (5, 16, 17, 1)]
+    vs = [torch.randn(n, 2, 8, generator=g) for n in (5, 16, 17, 1)]
+    Kc, Vc, pt = ra.build_paged_kv(ks, vs, page_size=4)
+    assert pt.dtype == torch.int32 and pt.shape == (4, 5)
+    assert Kc.shape == (2 + 4 + 5 + 1, 4, 2, 8)
+    for b, (k, v) in enumerate(zip(ks, vs)):
+        for c in range(k.shape[0]):
+            page = int(pt[b, c // 4])
+            assert torch.equal(Kc[page, c % 4], k[c]) and torch.equal(Vc[page, c % 4], v[c])
+
+
+@pytest.mark.parametrize("b,d", [(1, 5), (2, 3), (3, 3), (4, 2), (8, 2)])
+def test_tree_mask_module_matches_oracle(b, d):
+    assert tm.num_tree_nodes(b, d) == tree.num_tree_nodes(b, d)
+    assert tm.build_tree(b, d) == tree.build_tree(b, d)
+    assert (tm.tree_attention_mask(b, d) == tree.tree_attention_mask(b, d)).all()
+    n = num_tree_nodes(b, d)
+    assert (tm.tree_attention_mask_n(b, n - 1) == tree.tree_attention_mask_n(b, n - 1)).all()
+    assert tm.verify_tree_mask(b, d, verbose=False)
+    assert (tm.tree_attention_mask_pruned(tm.build_tree(b, d)) == tree.tree_attention_mask(b, d)).all()
+    fm = tm.full_sequence_mask(3, b, d)
+    assert fm.shape == (3 + n, 3 + n) and fm[3:, :3].all() and not fm[0, 1]
+
+
+def test_kernel_parents_self_loop():
+    p = tm.kernel_parents([-1, 0, 0, 1])
+    assert p.tolist() == [0, 0, 0, 1] and p.dtype == np.int32
+    cu = np.array([0, 4], dtype=np.int32)
+    assert (clib.ancestor_table_parents(cu, p, 3) == clib.ancestor_table_heap(cu, 2, 3)).all()
+
+
+def test_src_shim_reexports():
+    import src.ragged_attn as sra
+    import src.tree_mask as stm
+    for name in ("pack_inputs", "ragged_attention", "ragged_attention_with_lse", "ragged_attention_sibling",
+                 "ragged_attention_sibling_with_lse", "ragged_attention_with_parents",
+                 "ragged_attention_paged", "build_paged_kv", "fused_lse_merge"):
+        assert getattr(sra, name) is getattr(ra, name)
+    assert stm.tree_attention_mask is tm.tree_attention_mask
