@@ -138,6 +138,47 @@ int qattn_ancestors(const int32_t *cu_seqlens, const int32_t *parents, int32_t b
                     int32_t max_depth, int32_t *out, void *stream);
 
 /*
+ * Tree-verify attention with a prefix KV cache that every tree query attends
+ * in full, plus its own ancestors among the tree tokens.
+ *
+ * Replaces _ragged_attn_hybrid_kernel (src/ragged_attn.py:1709-1848) launched
+ * by ragged_attention_hybrid (:1851-1888), and the three-step caller pipeline
+ * "prefix flash attention + ragged_attention_with_lse + fused_lse_merge"
+ * (scripts/benchmark_micro.py:568-593, scripts/e2e_benchmark.py:1394-1502).
+ *
+ * Prefix key/value row j of sequence s, kv head g, is
+ *   k_prefix + s*kp_stride[0] + j*kp_stride[1] + g*kp_stride[2]
+ * (kp_stride[0] == 0 shares one prefix across the batch; K/V heads are GQA
+ * heads, never repeated).  Tree key/value row of local ancestor x of sequence
+ * s is  tree_seq_stride ? s*tree_seq_stride + tree_row0 + x : cu_seqlens[s] + x
+ * (the reference hybrid layout [B*(L+N), H, D] is tree_seq_stride = L+N,
+ * tree_row0 = L).  The prefix is computed with v_mfma_f32_16x16x32 in splits
+ * along the prefix; the split states are merged into the ancestor walk, which
+ * normalises once.  workspace (device, 256-byte aligned, at least
+ * qattn_prefix_workspace_bytes() bytes for the same sizes and num_splits)
+ * holds the split states; num_splits 0 picks a split count for 256 CUs.
+ * prefix_len 0 reduces to qattn_tree_fwd (workspace unused).
+ */
+int64_t qattn_prefix_workspace_bytes(int32_t batch, int32_t max_seqlen, int64_t total_tokens,
+                                     int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                                     int32_t prefix_len, int32_t num_splits);
+
+int qattn_prefix_tree_fwd(const void *q, const int64_t q_stride[3],
+                          const void *k, const int64_t k_stride[3],
+                          const void *v, const int64_t v_stride[3],
+                          const void *k_prefix, const int64_t kp_stride[3],
+                          const void *v_prefix, const int64_t vp_stride[3],
+                          int32_t prefix_len,
+                          void *o, const int64_t o_stride[3],
+                          float *lse, const int64_t lse_stride[2],
+                          const int32_t *cu_seqlens, int32_t batch, int32_t max_seqlen,
+                          int64_t total_tokens, int64_t tree_seq_stride, int64_t tree_row0,
+                          int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                          int32_t branching_factor, int32_t max_depth, float scale,
+                          int32_t dtype, void *workspace, int64_t workspace_size,
+                          int32_t num_splits, void *stream);
+
+/*
  * Two-state softmax merge.
  *
  * Replaces _fused_lse_merge_kernel (src/ragged_attn.py:1575-1616) launched by

@@ -94,5 +94,19 @@ struct SubtreePlan {
 };
 
 void set_error(const char* fmt, ...);
+void clear_error();
+
+// Host helpers shared by the entry points (tree_attn.hip).
+bool row_aligned(const void* ptr, const int64_t* st, int n_outer);
+int check_common(int32_t dtype, int32_t head_dim, int32_t batch, int32_t max_seqlen, int64_t total_tokens,
+                 int32_t hq, int32_t hkv, int32_t max_depth);
+int launch_status(const char* what);
+int fill_tree_params(TreeParams& p, const void* q, const int64_t* qs, const void* k, const int64_t* ks,
+                     const void* v, const int64_t* vs, void* o, const int64_t* os, float* lse, const int64_t* lss,
+                     const int32_t* cu, int32_t batch, int32_t max_seqlen, int64_t total_tokens, int32_t hq,
+                     int32_t hkv, int32_t b, int32_t max_depth, float scale);
+// walk: 0 heap, 1 parents; layout: 0 packed, 1 paged
+int run_tree(const TreeParams& p, int dtype, int head_dim, int walk, int layout, bool pstate, int algo,
+             hipStream_t st);
 
 }  // namespace qattn

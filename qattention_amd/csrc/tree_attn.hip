@@ -34,8 +34,17 @@ namespace qattn {
 
 constexpr int kThreads = 256;
 constexpr int kChunk = 8;          // ancestor steps whose loads are issued together
-constexpr int kLdsBudget = 48 * 1024;  // bytes of K+V rows staged per subtree tile
-constexpr int kMaxPass = 6;        // staging passes (kLdsBudget / (4 D) rows / (256 / (D/8)))
+#ifndef QATTN_SUBTREE_LDS_KB
+#define QATTN_SUBTREE_LDS_KB 48
+#endif
+#ifndef QATTN_SUBTREE_WAVES_PER_EU
+#define QATTN_SUBTREE_WAVES_PER_EU 3
+#endif
+// Bytes of K+V rows staged per subtree tile (a tuning constant: the tile size
+// trades workgroups per CU against ancestor rows re-read above each tile).
+constexpr int kLdsBudget = QATTN_SUBTREE_LDS_KB * 1024;
+// Staging passes: kLdsBudget / (4 D) rows, 256 / (D / 8) rows per pass.
+constexpr int kMaxPass = kLdsBudget / 8192;
 
 enum { WALK_HEAP = 0, WALK_PARENTS = 1 };
 enum { KV_PACKED = 0, KV_PAGED = 1 };
@@ -48,6 +57,8 @@ void set_error(const char* fmt, ...) {
     vsnprintf(g_err, sizeof(g_err), fmt, ap);
     va_end(ap);
 }
+
+void clear_error() { g_err[0] = 0; }
 
 // ---------------------------------------------------------------------------
 // Device helpers shared by the kernels
@@ -233,10 +244,139 @@ __global__ __launch_bounds__(kThreads) void tree_gather_kernel(TreeParams p) {
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ int rl(int v, int i) { return __builtin_amdgcn_readlane(v, i); }
 
+// Initial state from split-K partials for a 4-lane query group: lane j owns
+// the 16-byte chunks j, j+4, ... of the head row.
+template <int D>
+__device__ __forceinline__ void load_partial_state4(const TreeParams& p, int64_t qrow, int h, int j,
+                                                    float& m, float& l, float* acc) {
+    constexpr int NCH = D / 32;
+    const int64_t plane = p.total_tokens * (int64_t)p.Hq;
+    const int64_t idx = qrow * p.Hq + h;
+    float m0 = -INFINITY;
+    for (int s = 0; s < p.n_split; ++s) m0 = fmaxf(m0, p.part_m[s * plane + idx]);
+    m = m0;
+    l = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8 * NCH; ++e) acc[e] = 0.f;
+    if (m0 == -INFINITY) return;
+    for (int s = 0; s < p.n_split; ++s) {
+        const float w = fast_exp2(p.part_m[s * plane + idx] - m0);
+        l = __builtin_fmaf(w, p.part_l[s * plane + idx], l);
+        const float* a = p.part_acc + (s * plane + idx) * D + 8 * j;
+#pragma unroll
+        for (int i = 0; i < NCH; ++i) {
+            const float4 a0 = *reinterpret_cast<const float4*>(a + 32 * i);
+            const float4 a1 = *reinterpret_cast<const float4*>(a + 32 * i + 4);
+            float* c = acc + 8 * i;
+            c[0] = __builtin_fmaf(w, a0.x, c[0]);
+            c[1] = __builtin_fmaf(w, a0.y, c[1]);
+            c[2] = __builtin_fmaf(w, a0.z, c[2]);
+            c[3] = __builtin_fmaf(w, a0.w, c[3]);
+            c[4] = __builtin_fmaf(w, a1.x, c[4]);
+            c[5] = __builtin_fmaf(w, a1.y, c[5]);
+            c[6] = __builtin_fmaf(w, a1.z, c[6]);
+            c[7] = __builtin_fmaf(w, a1.w, c[7]);
+        }
+    }
+}
+
+// Exactly NS consecutive ancestor steps of one query, straight-line so the
+// scheduler can issue every LDS read of the chunk ahead of its use: scores
+// first, then one max, then the exponentials and the V accumulation
+// (two-phase softmax), merged into (m, l, acc) online.
+template <typename T, int D, int NS>
+__device__ __forceinline__ void fold_chunk(const uint16_t* Ks, const uint16_t* Vs, const Vec16* qf, int32_t& cur,
+                                           int lam_t0, int off, int lam_min, const Divider& bdiv, float c, int j,
+                                           float& m, float& l, float* acc) {
+    constexpr int NCH = D / 32;
+    int rows[NS];
+    float s[NS];
+#pragma unroll
+    for (int t = 0; t < NS; ++t) {
+        rows[t] = cur + rl(off, lam_t0 - t - lam_min);
+        cur = heap_parent(cur, bdiv);
+    }
+#pragma unroll
+    for (int t = 0; t < NS; ++t) {
+        const uint16_t* kr = Ks + (size_t)rows[t] * D + 8 * j;
+        float d = 0.f;
+#pragma unroll
+        for (int i = 0; i < NCH; ++i) d += dot8<T>(qf[i], ld16(kr + 32 * i));
+        s[t] = group_sum<4>(d) * c;
+    }
+    float cm = s[0];
+#pragma unroll
+    for (int t = 1; t < NS; ++t) cm = fmaxf(cm, s[t]);
+    const float m_new = fmaxf(m, cm);
+    if (m != -INFINITY) {
+        const float alpha = fast_exp2(m - m_new);
+        l *= alpha;
+#pragma unroll
+        for (int e = 0; e < 8 * NCH; ++e) acc[e] *= alpha;
+    }
+#pragma unroll
+    for (int t = 0; t < NS; ++t) {
+        const float pt = fast_exp2(s[t] - m_new);
+        l += pt;
+        const uint16_t* vr = Vs + (size_t)rows[t] * D + 8 * j;
+#pragma unroll
+        for (int i = 0; i < NCH; ++i) axpy8<T>(acc + 8 * i, pt, ld16(vr + 32 * i));
+    }
+    m = m_new;
+}
+
+// One query of a subtree tile: walk nsteps ancestors (all staged in LDS) in
+// chunks of at most 8 steps.  Level offsets: the LDS row of node x at level mu
+// is x + off[mu - lam_min] (one level per lane; mu is wave-uniform, so the
+// lookup is a readlane).  nsteps is wave-uniform, so the switch is a scalar
+// branch.
+template <typename T, int D>
+__device__ __forceinline__ void subtree_query(const uint16_t* Ks, const uint16_t* Vs, const Vec16* qf, int node,
+                                              int lam, int nsteps, int off, int lam_min, const Divider& bdiv,
+                                              float c, int j, float& m, float& l, float* acc) {
+    int32_t cur = node;
+    for (int t0 = 0; t0 < nsteps; t0 += 8) {
+        const int cnt = (nsteps - t0 < 8) ? nsteps - t0 : 8;
+        const int lt = lam - t0;
+        switch (cnt) {
+            case 1: fold_chunk<T, D, 1>(Ks, Vs, qf, cur, lt, off, lam_min, bdiv, c, j, m, l, acc); break;
+            case 2: fold_chunk<T, D, 2>(Ks, Vs, qf, cur, lt, off, lam_min, bdiv, c, j, m, l, acc); break;
+            case 3: fold_chunk<T, D, 3>(Ks, Vs, qf, cur, lt, off, lam_min, bdiv, c, j, m, l, acc); break;
+            case 4: fold_chunk<T, D, 4>(Ks, Vs, qf, cur, lt, off, lam_min, bdiv, c, j, m, l, acc); break;
+            case 5: fold_chunk<T, D, 5>(Ks, Vs, qf, cur, lt, off, lam_min, bdiv, c, j, m, l, acc); break;
+            case 6: fold_chunk<T, D, 6>(Ks, Vs, qf, cur, lt, off, lam_min, bdiv, c, j, m, l, acc); break;
+            case 7: fold_chunk<T, D, 7>(Ks, Vs, qf, cur, lt, off, lam_min, bdiv, c, j, m, l, acc); break;
+            default: fold_chunk<T, D, 8>(Ks, Vs, qf, cur, lt, off, lam_min, bdiv, c, j, m, l, acc); break;
+        }
+    }
+}
+
+template <typename T, int D, bool LSE>
+__device__ __forceinline__ void write_out4(const TreeParams& p, int64_t qrow, int h, int j, float m, float l,
+                                           float* acc) {
+    constexpr int NCH = D / 32;
+    const float l_safe = (l == 0.f) ? 1.f : l;
+    const float inv = __builtin_amdgcn_rcpf(l_safe);
+    uint16_t* optr = (uint16_t*)p.o + qrow * p.so_t + (int64_t)h * p.so_h + 8 * j;
+#pragma unroll
+    for (int i = 0; i < NCH; ++i) {
+        float r[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) r[e] = acc[8 * i + e] * inv;
+        st16(optr + 32 * i, pack8<T>(r));
+    }
+    if constexpr (LSE) {
+        if (j == 0) p.lse[qrow * p.slse_t + (int64_t)h * p.slse_h] = (m + fast_log2(l_safe)) * kLn2;
+    }
+}
+
+// At most 3 workgroups of 48 KB LDS fit a CU, so the register budget may be
+// sized for 3 waves per SIMD (up to 168 VGPRs) to keep more LDS reads in flight.
 template <typename T, int D, bool LSE, bool PSTATE>
-__global__ __launch_bounds__(kThreads) void tree_subtree_kernel(TreeParams p, SubtreePlan plan, Divider gdiv) {
-    constexpr int LPR = D / 8;
-    constexpr int SLOTS = kThreads / LPR;  // row groups per workgroup
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, QATTN_SUBTREE_WAVES_PER_EU))) void tree_subtree_kernel(TreeParams p, SubtreePlan plan, Divider gdiv) {
+    constexpr int LPR = D / 8;             // staging: lanes per 16-byte-vector row
+    constexpr int SLOTS = kThreads / LPR;  // staging: rows per pass
+    constexpr int NCH = D / 32;            // compute: 16-byte chunks per lane (4 lanes per query)
     extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
     uint16_t* Ks = smem;
     uint16_t* Vs = smem + (size_t)plan.max_rows * D;
@@ -293,9 +433,9 @@ __global__ __launch_bounds__(kThreads) void tree_subtree_kernel(TreeParams p, Su
         const int lam = lam_min + lane64;
         int64_t f, la;
         if (lam >= lo) {
-            const int j = lam - lo;
+            const int jj = lam - lo;
             int64_t bj = 1, sj = 0;
-            for (int i = 0; i < j; ++i) {
+            for (int i = 0; i < jj; ++i) {
                 sj += bj;
                 bj *= b;
             }
@@ -352,18 +492,41 @@ __global__ __launch_bounds__(kThreads) void tree_subtree_kernel(TreeParams p, Su
         }
     }
 
-    // ---- query cursor: levels lo..hi, SLOTS (node, q head) pairs per pass ---
+    // ---- query schedule: 16 (node, q head) pairs per wave item; a wave item
+    // never spans two levels, so its step count is wave-uniform -----------------
     const int g = p.group;
-    int lam = lo, s0 = 0;
-    auto level_items = [&](int L) -> int { return (L <= hi) ? rl(cnt, L - lam_min) * g : 0; };
-    auto load_q = [&](int L, int s, Vec16& dst) {
-        const int node = rl(first, L - lam_min) + divide(s, gdiv);
-        const int qh = kvh * g + (s - divide(s, gdiv) * g);
-        dst = ld16((const uint16_t*)p.q + ((int64_t)start + node) * p.sq_t + (int64_t)qh * p.sq_h + lane * 8);
+    // readfirstlane tells the compiler the wave index is wave-uniform, which
+    // keeps the whole query schedule (levels, step counts) in scalar registers
+    // and the ancestor loop free of divergent branches.
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int grp = lane64 >> 2;
+    const int j = lane64 & 3;
+    const int lam_l = lam_min + lane64;
+    const int nw = (lane64 < nlev && lam_l >= lo) ? (cnt * g + 15) / 16 : 0;  // wave items per level
+    auto advance = [&](int& L, int& k) {
+        while (L <= hi) {
+            const int w = rl(nw, L - lam_min);
+            if (k < w) break;
+            k -= w;
+            ++L;
+        }
     };
-    Vec16 qcur = Vec16{{0u, 0u, 0u, 0u}}, qnext = Vec16{{0u, 0u, 0u, 0u}};
-    int items = level_items(lam);
-    if (rg < items) load_q(lam, rg, qcur);
+    auto load_q = [&](int L, int k, Vec16* dst) {
+        const int s = k * 16 + grp;
+        if (s < rl(cnt, L - lam_min) * g) {
+            const int node = rl(first, L - lam_min) + divide(s, gdiv);
+            const int qh = kvh * g + (s - divide(s, gdiv) * g);
+            const uint16_t* qp = (const uint16_t*)p.q + ((int64_t)start + node) * p.sq_t + (int64_t)qh * p.sq_h + 8 * j;
+#pragma unroll
+            for (int i = 0; i < NCH; ++i) dst[i] = ld16(qp + 32 * i);
+        }
+    };
+    int L = lo, k = wave;
+    advance(L, k);
+    Vec16 qcur[NCH], qnext[NCH];
+#pragma unroll
+    for (int i = 0; i < NCH; ++i) qcur[i] = qnext[i] = Vec16{{0u, 0u, 0u, 0u}};
+    if (L <= hi) load_q(L, k, qcur);
 
 #pragma unroll
     for (int ps = 0; ps < kMaxPass; ++ps) {
@@ -375,61 +538,34 @@ __global__ __launch_bounds__(kThreads) void tree_subtree_kernel(TreeParams p, Su
     }
     __syncthreads();
 
-    while (lam <= hi && items > 0) {
-        // next cursor position and its Q prefetch
-        int lam_n = lam, s0_n = s0 + SLOTS, items_n = items;
-        if (s0_n >= items) {
-            lam_n = lam + 1;
-            s0_n = 0;
-            items_n = level_items(lam_n);
-        }
-        if (s0_n + rg < items_n) load_q(lam_n, s0_n + rg, qnext);
+    while (L <= hi) {
+        int Ln = L, kn = k + kThreads / 64;
+        advance(Ln, kn);
+        if (Ln <= hi) load_q(Ln, kn, qnext);
 
-        const int s = s0 + rg;
-        if (s < items) {
-            const int node = rl(first, lam - lam_min) + divide(s, gdiv);
+        const int s = k * 16 + grp;
+        if (s < rl(cnt, L - lam_min) * g) {
+            const int node = rl(first, L - lam_min) + divide(s, gdiv);
             const int qh = kvh * g + (s - divide(s, gdiv) * g);
             const int64_t qrow = (int64_t)start + node;
-            float m = -INFINITY, l = 0.f, acc[8];
+            float m = -INFINITY, l = 0.f, acc[8 * NCH];
             if constexpr (PSTATE) {
-                load_partial_state<D>(p, qrow, qh, lane, m, l, acc);
+                load_partial_state4<D>(p, qrow, qh, j, m, l, acc);
             } else {
 #pragma unroll
-                for (int j = 0; j < 8; ++j) acc[j] = 0.f;
+                for (int e = 0; e < 8 * NCH; ++e) acc[e] = 0.f;
             }
-            // steps t = 0..min(lam, max_depth) attend levels lam - t; the heap
-            // walk strictly decreases until the root, so these are exactly the
-            // steps with c_t != c_{t-1} (src/ragged_attn.py:338-377).
-            const int nsteps = (lam < p.max_depth ? lam : p.max_depth) + 1;
-            int32_t cur = node;
-            for (int t0 = 0; t0 < nsteps; t0 += kChunk) {
-                Vec16 kr[kChunk], vr[kChunk];
-                bool val[kChunk];
-#pragma unroll
-                for (int j = 0; j < kChunk; ++j) {
-                    const int t = t0 + j;
-                    val[j] = t < nsteps;
-                    const int mu = lam - t;
-                    const int row = cur + rl(off, (val[j] ? mu : lam) - lam_min);
-                    const int rrow = val[j] ? row : 0;
-                    kr[j] = ld16(Ks + (size_t)rrow * D + lane * 8);
-                    vr[j] = ld16(Vs + (size_t)rrow * D + lane * 8);
-                    cur = heap_parent(cur, p.bdiv);
-                }
-                float sc[kChunk];
-#pragma unroll
-                for (int j = 0; j < kChunk; ++j) {
-                    const float d = group_sum<LPR>(dot8<T>(qcur, kr[j])) * p.scale_log2;
-                    sc[j] = val[j] ? d : -INFINITY;
-                }
-                softmax_fold<T, kChunk>(m, l, acc, sc, vr);
-            }
-            write_out<T, LSE>(p, qrow, qh, lane, m, l, acc);
+            // steps t = 0..min(L, max_depth) attend levels L - t; the heap walk
+            // strictly decreases until the root, so these are exactly the steps
+            // with c_t != c_{t-1} (src/ragged_attn.py:338-377).
+            const int nsteps = (L < p.max_depth ? L : p.max_depth) + 1;
+            subtree_query<T, D>(Ks, Vs, qcur, node, L, nsteps, off, lam_min, p.bdiv, p.scale_log2, j, m, l, acc);
+            write_out4<T, D, LSE>(p, qrow, qh, j, m, l, acc);
         }
-        qcur = qnext;
-        lam = lam_n;
-        s0 = s0_n;
-        items = items_n;
+#pragma unroll
+        for (int i = 0; i < NCH; ++i) qcur[i] = qnext[i];
+        L = Ln;
+        k = kn;
     }
 }
 
@@ -494,14 +630,14 @@ __global__ __launch_bounds__(kThreads) void lse_merge_kernel(MergeParams mp) {
 // ---------------------------------------------------------------------------
 // Host side: validation, planning, dispatch
 // ---------------------------------------------------------------------------
-static bool row_aligned(const void* ptr, const int64_t* st, int n_outer) {
+bool row_aligned(const void* ptr, const int64_t* st, int n_outer) {
     if (((uintptr_t)ptr & 15u) != 0) return false;
     for (int i = 0; i < n_outer; ++i)
         if (st[i] % 8 != 0) return false;
     return st[n_outer] == 1;
 }
 
-static int check_common(int32_t dtype, int32_t head_dim, int32_t batch, int32_t max_seqlen,
+int check_common(int32_t dtype, int32_t head_dim, int32_t batch, int32_t max_seqlen,
                         int64_t total_tokens, int32_t hq, int32_t hkv, int32_t max_depth) {
     if (dtype != QATTN_DTYPE_F16 && dtype != QATTN_DTYPE_BF16) {
         set_error("dtype %d is not fp16 (0) or bf16 (1)", dtype);
@@ -524,7 +660,7 @@ static int check_common(int32_t dtype, int32_t head_dim, int32_t batch, int32_t 
     return QATTN_OK;
 }
 
-static int launch_status(const char* what) {
+int launch_status(const char* what) {
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
         set_error("%s: %s", what, hipGetErrorString(e));
@@ -779,9 +915,14 @@ int qattn_tree_fwd(const void* q, const int64_t q_stride[3], const void* k, cons
                    int64_t total_tokens, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
                    int32_t branching_factor, int32_t max_depth, float scale, int32_t dtype, int32_t algo,
                    void* stream) {
-    g_err[0] = 0;
+    clear_error();
     int rc = check_common(dtype, head_dim, batch, max_seqlen, total_tokens, num_q_heads, num_kv_heads, max_depth);
     if (rc) return rc;
+    if (algo < QATTN_ALGO_AUTO || algo > QATTN_ALGO_SUBTREE) {
+        set_error("unknown algo %d", algo);
+        return QATTN_ERR_ARG;
+    }
+    if (batch == 0 || max_seqlen == 0 || total_tokens == 0) return QATTN_OK;  // nothing to compute
     TreeParams p;
     rc = fill_tree_params(p, q, q_stride, k, k_stride, v, v_stride, o, o_stride, lse, lse_stride, cu_seqlens,
                           batch, max_seqlen, total_tokens, num_q_heads, num_kv_heads, branching_factor, max_depth,
@@ -791,11 +932,6 @@ int qattn_tree_fwd(const void* q, const int64_t q_stride[3], const void* k, cons
         set_error("k/v rows must be 16-byte aligned with stride_dim 1");
         return QATTN_ERR_LAYOUT;
     }
-    if (algo < QATTN_ALGO_AUTO || algo > QATTN_ALGO_SUBTREE) {
-        set_error("unknown algo %d", algo);
-        return QATTN_ERR_ARG;
-    }
-    if (batch == 0 || max_seqlen == 0 || total_tokens == 0) return QATTN_OK;
     return run_tree(p, dtype, head_dim, WALK_HEAP, KV_PACKED, false, algo, (hipStream_t)stream);
 }
 
@@ -805,9 +941,10 @@ int qattn_tree_parents_fwd(const void* q, const int64_t q_stride[3], const void*
                            const int32_t* parents, int32_t batch, int32_t max_seqlen, int64_t total_tokens,
                            int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, int32_t max_depth,
                            float scale, int32_t dtype, void* stream) {
-    g_err[0] = 0;
+    clear_error();
     int rc = check_common(dtype, head_dim, batch, max_seqlen, total_tokens, num_q_heads, num_kv_heads, max_depth);
     if (rc) return rc;
+    if (batch == 0 || max_seqlen == 0 || total_tokens == 0) return QATTN_OK;  // nothing to compute
     if (!parents) {
         set_error("parents is null");
         return QATTN_ERR_ARG;
@@ -821,7 +958,6 @@ int qattn_tree_parents_fwd(const void* q, const int64_t q_stride[3], const void*
         return QATTN_ERR_LAYOUT;
     }
     p.parents = parents;
-    if (batch == 0 || max_seqlen == 0 || total_tokens == 0) return QATTN_OK;
     return run_tree(p, dtype, head_dim, WALK_PARENTS, KV_PACKED, false, QATTN_ALGO_GATHER, (hipStream_t)stream);
 }
 
@@ -832,9 +968,10 @@ int qattn_tree_paged_fwd(const void* q, const int64_t q_stride[3], const void* k
                          int32_t batch, int32_t max_seqlen, int64_t total_tokens, int32_t num_q_heads,
                          int32_t num_kv_heads, int32_t head_dim, int32_t branching_factor, int32_t max_depth,
                          float scale, int32_t dtype, void* stream) {
-    g_err[0] = 0;
+    clear_error();
     int rc = check_common(dtype, head_dim, batch, max_seqlen, total_tokens, num_q_heads, num_kv_heads, max_depth);
     if (rc) return rc;
+    if (batch == 0 || max_seqlen == 0 || total_tokens == 0) return QATTN_OK;  // nothing to compute
     if (!page_table || !k_stride || !v_stride || page_size < 1 || pt_cols < 0 || num_pages < 0) {
         set_error("bad paged arguments: page_size=%d pt_cols=%d num_pages=%d", page_size, pt_cols, num_pages);
         return QATTN_ERR_ARG;
@@ -857,14 +994,13 @@ int qattn_tree_paged_fwd(const void* q, const int64_t q_stride[3], const void* k
     p.page_size = page_size;
     p.sk_page = k_stride[0];
     p.sv_page = v_stride[0];
-    if (batch == 0 || max_seqlen == 0 || total_tokens == 0) return QATTN_OK;
     return run_tree(p, dtype, head_dim, WALK_HEAP, KV_PAGED, false, QATTN_ALGO_GATHER, (hipStream_t)stream);
 }
 
 int qattn_ancestors(const int32_t* cu_seqlens, const int32_t* parents, int32_t batch, int32_t max_seqlen,
                     int64_t total_tokens, int32_t branching_factor, int32_t max_depth, int32_t* out,
                     void* stream) {
-    g_err[0] = 0;
+    clear_error();
     if (!cu_seqlens || !out || batch < 0 || max_seqlen < 0 || total_tokens < 0 || max_depth < 0 ||
         (!parents && branching_factor < 1) || total_tokens >= (int64_t(1) << 31)) {
         set_error("bad arguments to qattn_ancestors");
@@ -894,7 +1030,7 @@ int qattn_lse_merge(const float* lse_pre, const int64_t lse_pre_stride[3], const
                     const int64_t lse_tree_stride[3], const void* o_pre, const int64_t o_pre_stride[4],
                     const void* o_tree, const int64_t o_tree_stride[4], void* out, const int64_t out_stride[4],
                     int32_t B, int32_t H, int32_t Nq, int32_t head_dim, int32_t dtype, void* stream) {
-    g_err[0] = 0;
+    clear_error();
     if (!lse_pre || !lse_tree || !o_pre || !o_tree || !out || !lse_pre_stride || !lse_tree_stride ||
         !o_pre_stride || !o_tree_stride || !out_stride || B < 0 || H < 0 || Nq < 0) {
         set_error("bad arguments to qattn_lse_merge");

@@ -327,6 +327,117 @@ def build_paged_kv(
     return K_cache, V_cache, page_table
 
 
+def _prefix_tree_forward(Q, K, V, cu_dev, B: int, max_seqlen: int, Kp, kp_stride, Vp, vp_stride,
+                         prefix_len: int, branching_factor: int, max_depth: int, tree_seq_stride: int,
+                         tree_row0: int, want_lse: bool, num_splits: int = 0):
+    """Launch qattn_prefix_tree_fwd: MFMA prefix splits + ancestor walk, one
+    normalisation.  K/V hold the tree rows (addressed through cu_dev or
+    tree_seq_stride/tree_row0); Kp/Vp + 3 strides address the prefix rows."""
+    device = Q.device
+    T, Hq, D = Q.shape
+    Hkv = K.shape[1]
+    O = torch.empty_like(Q)
+    if not _vec_ok(O):
+        O = torch.empty(Q.shape, dtype=Q.dtype, device=device)
+    LSE = torch.empty(T, Hq, dtype=torch.float32, device=device) if want_lse else None
+    L = _lib.lib()
+    ws_bytes = int(L.qattn_prefix_workspace_bytes(B, max_seqlen, T, Hq, Hkv, D, int(prefix_len), int(num_splits)))
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=device)
+    with torch.cuda.device(device):
+        rc = L.qattn_prefix_tree_fwd(
+            Q.data_ptr(), _lib.i64arr(Q.stride()), K.data_ptr(), _lib.i64arr(K.stride()),
+            V.data_ptr(), _lib.i64arr(V.stride()), _lib.ptr(Kp), _lib.i64arr(kp_stride),
+            _lib.ptr(Vp), _lib.i64arr(vp_stride), int(prefix_len),
+            O.data_ptr(), _lib.i64arr(O.stride()), _lib.ptr(LSE),
+            _lib.i64arr(LSE.stride()) if LSE is not None else None,
+            cu_dev.data_ptr(), B, max_seqlen, T, int(tree_seq_stride), int(tree_row0),
+            Hq, Hkv, D, int(branching_factor), int(max_depth), 1.0 / math.sqrt(D), _dtype_code(Q),
+            ws.data_ptr(), ws_bytes, int(num_splits), _stream(device))
+    _lib.check(rc, "qattn_prefix_tree_fwd")
+    return O, LSE
+
+
+def ragged_attention_hybrid(
+    Q: torch.Tensor,
+    K: torch.Tensor,
+    V: torch.Tensor,
+    prefix_length: int,
+    tree_size: int,
+    branching_factor: int,
+    max_depth: int,
+) -> torch.Tensor:
+    """Dense prefix + ancestor-sparse tree in one state (src/ragged_attn.py:1851-1888).
+
+    Q: [B*N, H, D]; K, V: [B*(L+N), Hkv, D] with each sequence's L prefix rows
+    followed by its N tree rows (Hkv may divide H: GQA).  Every query attends
+    all L prefix rows of its sequence plus its tree ancestors."""
+    _check_dtypes(Q, K, V)
+    device = _require_device(Q, K, V)
+    T, Hq, Hkv, D = _heads(Q, K, V)
+    N, L = int(tree_size), int(prefix_length)
+    if N <= 0 or T % N:
+        raise ValueError(f"Q has {T} rows, not a multiple of tree_size {N}")
+    B = T // N
+    if K.shape[0] != B * (L + N) or V.shape[0] != B * (L + N):
+        raise ValueError(f"K/V must have B*(L+N) = {B * (L + N)} rows (got {K.shape[0]})")
+    Q, K, V = _vec(Q), _vec(K), _vec(V)
+    cu = torch.arange(0, (B + 1) * N, N, dtype=torch.int32, device=device)
+    kp_stride = (K.stride(0) * (L + N), K.stride(0), K.stride(1))
+    vp_stride = (V.stride(0) * (L + N), V.stride(0), V.stride(1))
+    return _prefix_tree_forward(Q, K, V, cu, B, N, K if L else None, kp_stride, V if L else None, vp_stride,
+                                L, branching_factor, max_depth, L + N, L, False)[0]
+
+
+def ragged_attention_prefix(
+    Q: torch.Tensor,
+    K: torch.Tensor,
+    V: torch.Tensor,
+    cu_seqlens: torch.Tensor,
+    K_prefix: torch.Tensor,
+    V_prefix: torch.Tensor,
+    branching_factor: int,
+    max_depth: int,
+    max_seqlen: int = None,
+    return_lse: bool = False,
+    num_splits: int = 0,
+):
+    """Tree-verify attention over a prefix KV cache, GQA-native, in one pass.
+
+    Replaces the reference's verify pipeline "prefix flash attention with LSE +
+    ragged_attention_with_lse + fused_lse_merge" (scripts/benchmark_micro.py:568-593,
+    scripts/e2e_benchmark.py:1394-1502) without repeat_kv and without the
+    intermediate O/LSE round trips.
+
+    Q: packed [T, Hq, D]; K, V: packed tree rows [T, Hkv, D]; cu_seqlens [B+1];
+    K_prefix, V_prefix: [B, L, Hkv, D] per-sequence or [L, Hkv, D] shared by
+    all sequences, any strides with a unit last dim (e.g. a permuted view of a
+    [B, Hkv, L, D] cache).  Returns O (and LSE [T, Hq] if return_lse)."""
+    _check_dtypes(Q, K, V)
+    assert K_prefix.dtype == Q.dtype and V_prefix.dtype == Q.dtype, "prefix dtype must match Q"
+    device = _require_device(Q, K, V, K_prefix, V_prefix)
+    T, Hq, Hkv, D = _heads(Q, K, V)
+    if K.shape[0] != T or V.shape[0] != T:
+        raise ValueError("packed Q, K, V must have the same number of tokens")
+    B = int(cu_seqlens.shape[0]) - 1
+    if K_prefix.dim() == 3:
+        K_prefix, V_prefix = K_prefix.unsqueeze(0), V_prefix.unsqueeze(0)
+        shared = True
+    else:
+        shared = False
+    if K_prefix.shape != V_prefix.shape or K_prefix.shape[2:] != (Hkv, D) or (not shared and K_prefix.shape[0] != B):
+        raise ValueError(f"prefix shape {tuple(K_prefix.shape)} incompatible with B={B}, Hkv={Hkv}, D={D}")
+    L = int(K_prefix.shape[1])
+    ms, cu_dev = _seqlens(cu_seqlens, B, device, max_seqlen)
+    Q, K, V = _vec(Q), _vec(K), _vec(V)
+    K_prefix, V_prefix = _vec(K_prefix), _vec(V_prefix)
+    kp_stride = (0 if shared else K_prefix.stride(0), K_prefix.stride(1), K_prefix.stride(2))
+    vp_stride = (0 if shared else V_prefix.stride(0), V_prefix.stride(1), V_prefix.stride(2))
+    O, LSE = _prefix_tree_forward(Q, K, V, cu_dev, B, ms, K_prefix if L else None, kp_stride,
+                                  V_prefix if L else None, vp_stride, L, branching_factor, max_depth, 0, 0,
+                                  return_lse, num_splits)
+    return (O, LSE) if return_lse else O
+
+
 def fused_lse_merge(
     lse_pre: torch.Tensor,
     lse_tree: torch.Tensor,

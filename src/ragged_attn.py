@@ -6,7 +6,9 @@ from qattention_amd.ragged_attn import (  # noqa: F401
     fused_lse_merge,
     pack_inputs,
     ragged_attention,
+    ragged_attention_hybrid,
     ragged_attention_paged,
+    ragged_attention_prefix,
     ragged_attention_sibling,
     ragged_attention_sibling_with_lse,
     ragged_attention_with_lse,

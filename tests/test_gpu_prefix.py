@@ -1,0 +1,248 @@
+"""GPU parity of the prefix (hybrid) path: MFMA prefix splits merged into the
+ancestor walk, against the pinned oracle.
+
+Tolerances: fp16 max |o - o_ref| <= 2e-3 plus the reference's
+allclose(atol=rtol=1e-2); bf16 half an ulp of max(1, |o_ref|) plus 2^-8
+relative for the probabilities the reference also rounds to bf16
+(src/ragged_attn.py:1797); LSE max abs <= 1e-4 (fp16) / 2e-3 (bf16).
+"""
+from __future__ import annotations
+
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import GOLDEN_DIR, make_inputs, num_tree_nodes, oracle_tree, tree_case
+from oracle import sdpa
+from oracle import clib
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+def say(*a):
+    print(*a, flush=True)
+
+
+def _ra():
+    from qattention_amd import ragged_attn
+    return ragged_attn
+
+
+def check_fp16(o, o_ref, what=""):
+    err = float(np.abs(o - o_ref).max()) if o.size else 0.0
+    assert err <= 2e-3, f"{what}: max abs err {err:.3e}"
+    assert np.allclose(o, o_ref, atol=1e-2, rtol=1e-2), what
+
+
+def check_bf16(o, o_ref, what=""):
+    bound = 2.0 ** -7 * np.maximum(1.0, np.abs(o_ref)) + 1e-3
+    err = np.abs(o - o_ref)
+    assert (err <= bound).all(), f"{what}: bf16 err {err.max():.3e}"
+
+
+def _prefix(B, L, Hkv, D, seed, dtype=torch.float16, sigma=1.0):
+    g = torch.Generator().manual_seed(seed)
+    Kp = (torch.randn(B, L, Hkv, D, generator=g) * sigma).to(dtype)
+    Vp = (torch.randn(B, L, Hkv, D, generator=g) * sigma).to(dtype)
+    return Kp, Vp
+
+
+def _hybrid_layout(K, Kp, B, N):
+    """[B*(L+N), H, D]: each sequence's prefix rows then its tree rows."""
+    L = Kp.shape[1]
+    H, D = K.shape[1], K.shape[2]
+    out = torch.cat([Kp, K.view(B, N, H, D)], dim=1)
+    return out.reshape(B * (L + N), H, D).contiguous()
+
+
+# ---------------------------------------------------------------------------
+# ragged_attention_hybrid (the reference entry point, tests/test_correctness.py:402-469)
+# ---------------------------------------------------------------------------
+
+HYB_CONFIGS = [(1, 2, 3), (4, 2, 5), (4, 3, 5), (8, 2, 5), (8, 3, 5), (4, 4, 4), (2, 8, 3)]
+
+
+@pytest.mark.parametrize("B,b,d", HYB_CONFIGS)
+def test_hybrid_matches_reference_tests(B, b, d):
+    ra = _ra()
+    say("hybrid", B, b, d)
+    N = num_tree_nodes(b, d)
+    H, D = 4, 64
+    Q, K, V, cu = tree_case(B, b, d, H, D)
+    Qd, Kd, Vd = Q.to(DEV), K.to(DEV), V.to(DEV)
+    # L = 0 reduces to the tree-only kernel exactly
+    O0 = ra.ragged_attention_hybrid(Qd, Kd, Vd, 0, N, b, d)
+    assert torch.equal(O0, ra.ragged_attention(Qd, Kd, Vd, cu, b, d))
+    # L = 32 prefix columns attended by every query
+    L = 32
+    Kp, Vp = _prefix(B, L, H, D, B * 100 + b * 10 + d)
+    Kh, Vh = _hybrid_layout(K, Kp, B, N), _hybrid_layout(V, Vp, B, N)
+    O = ra.ragged_attention_hybrid(Qd, Kh.to(DEV), Vh.to(DEV), L, N, b, d)
+    o_ref, _, _ = oracle_tree(Q, K, V, cu, b, d, Kp=Kp, Vp=Vp)
+    check_fp16(O.double().cpu().numpy(), o_ref, "hybrid L=32")
+    # and the padded-SDPA restatement of the reference's own check (:444-469)
+    masks = [np.asarray(__import__("oracle.tree", fromlist=["x"]).tree_attention_mask(b, d))] * B
+    O_sdpa = sdpa.packed_tree_attention(Q, K, V, cu, masks, Kp=Kp, Vp=Vp)
+    assert torch.allclose(O.float().cpu(), O_sdpa, atol=1e-2, rtol=1e-2)
+
+
+def test_hybrid_gqa_and_long_prefix():
+    ra = _ra()
+    B, b, d, Hq, Hkv, D, L = 2, 4, 3, 8, 2, 128, 1000
+    N = num_tree_nodes(b, d)
+    Q, K, V, cu = tree_case(B, b, d, Hq, D, Hkv=Hkv)
+    Kp, Vp = _prefix(B, L, Hkv, D, 77)
+    O = ra.ragged_attention_hybrid(Q.to(DEV), _hybrid_layout(K, Kp, B, N).to(DEV),
+                                   _hybrid_layout(V, Vp, B, N).to(DEV), L, N, b, d)
+    o_ref, _, _ = oracle_tree(Q, K, V, cu, b, d, Kp=Kp, Vp=Vp)
+    check_fp16(O.double().cpu().numpy(), o_ref, "hybrid gqa")
+
+
+def test_golden_prefix_fixture():
+    ra = _ra()
+    z = np.load(os.path.join(GOLDEN_DIR, "prefix.npz"))
+    Q, K, V = (torch.from_numpy(z[n]).to(DEV) for n in ("q", "k", "v"))
+    Kp, Vp = (torch.from_numpy(z[n]).to(DEV) for n in ("kp", "vp"))
+    cu = torch.from_numpy(z["cu"])
+    O, L = ra.ragged_attention_prefix(Q, K, V, cu, Kp, Vp, int(z["b"]), int(z["max_depth"]), return_lse=True)
+    check_fp16(O.double().cpu().numpy(), z["o"].astype(np.float64), "prefix fixture")
+    assert np.abs(L.double().cpu().numpy() - z["lse"]).max() <= 1e-4
+
+
+# ---------------------------------------------------------------------------
+# ragged_attention_prefix (GQA-native verify with a prefix cache)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("Hq,Hkv,D,L,lens,b,md", [
+    (8, 2, 128, 200, [85, 85], 4, 3),
+    (4, 4, 64, 64, [15, 15, 15], 2, 3),
+    (4, 1, 32, 130, [31, 7], 2, 4),
+    (32, 8, 128, 777, [21, 85], 4, 3),
+    (6, 3, 64, 1, [40, 1, 13], 3, 2),
+    (2, 2, 128, 4096, [63], 2, 5),
+])
+def test_prefix_api(Hq, Hkv, D, L, lens, b, md):
+    ra = _ra()
+    say("prefix", Hq, Hkv, D, L, lens)
+    Q, K, V, cu = make_inputs(lens, Hq, D, 555 + L, Hkv=Hkv)
+    Kp, Vp = _prefix(len(lens), L, Hkv, D, 556 + L)
+    O, LSE = ra.ragged_attention_prefix(Q.to(DEV), K.to(DEV), V.to(DEV), cu, Kp.to(DEV), Vp.to(DEV), b, md,
+                                        return_lse=True)
+    o_ref, lse_ref, _ = oracle_tree(Q, K, V, cu, b, md, Kp=Kp, Vp=Vp)
+    check_fp16(O.double().cpu().numpy(), o_ref, "prefix api")
+    assert np.abs(LSE.double().cpu().numpy() - lse_ref).max() <= 1e-4
+
+
+def test_prefix_split_counts_agree():
+    """Any split count gives the same function (split states merge exactly up
+    to fp32 rounding)."""
+    ra = _ra()
+    Q, K, V, cu = make_inputs([85, 85], 8, 128, 909, Hkv=2)
+    Kp, Vp = _prefix(2, 1500, 2, 128, 910)
+    o_ref, _, _ = oracle_tree(Q, K, V, cu, 4, 3, Kp=Kp, Vp=Vp)
+    args = (Q.to(DEV), K.to(DEV), V.to(DEV), cu, Kp.to(DEV), Vp.to(DEV), 4, 3)
+    for ns in (1, 2, 5, 24, 0):
+        say("splits", ns)
+        O = ra.ragged_attention_prefix(*args, num_splits=ns)
+        check_fp16(O.double().cpu().numpy(), o_ref, f"splits={ns}")
+
+
+def test_prefix_shared_and_strided():
+    """A prefix shared by the batch ([L, Hkv, D]) and a permuted view of a
+    [B, Hkv, L, D] cache (the HF layout)."""
+    ra = _ra()
+    B, Hq, Hkv, D, L = 3, 8, 4, 64, 300
+    Q, K, V, cu = make_inputs([21, 21, 21], Hq, D, 31, Hkv=Hkv)
+    Kp, Vp = _prefix(1, L, Hkv, D, 32)
+    O = ra.ragged_attention_prefix(Q.to(DEV), K.to(DEV), V.to(DEV), cu, Kp[0].to(DEV), Vp[0].to(DEV), 4, 2)
+    o_ref, _, _ = oracle_tree(Q, K, V, cu, 4, 2, Kp=Kp.expand(B, -1, -1, -1), Vp=Vp.expand(B, -1, -1, -1))
+    check_fp16(O.double().cpu().numpy(), o_ref, "shared prefix")
+    Kp3, Vp3 = _prefix(B, L, Hkv, D, 33)
+    Kh = Kp3.permute(0, 2, 1, 3).contiguous().to(DEV).permute(0, 2, 1, 3)  # [B, L, Hkv, D] view of [B, Hkv, L, D]
+    Vh = Vp3.permute(0, 2, 1, 3).contiguous().to(DEV).permute(0, 2, 1, 3)
+    assert Kh.stride(1) == D
+    O = ra.ragged_attention_prefix(Q.to(DEV), K.to(DEV), V.to(DEV), cu, Kh, Vh, 4, 2)
+    o_ref, _, _ = oracle_tree(Q, K, V, cu, 4, 2, Kp=Kp3, Vp=Vp3)
+    check_fp16(O.double().cpu().numpy(), o_ref, "HF-layout prefix")
+
+
+def test_prefix_bf16():
+    ra = _ra()
+    Q, K, V, cu = make_inputs([85, 40], 8, 128, 71, dtype=torch.bfloat16, Hkv=2)
+    Kp, Vp = _prefix(2, 500, 2, 128, 72, dtype=torch.bfloat16)
+    O, LSE = ra.ragged_attention_prefix(Q.to(DEV), K.to(DEV), V.to(DEV), cu, Kp.to(DEV), Vp.to(DEV), 4, 3,
+                                        return_lse=True)
+    o_ref, lse_ref, _ = oracle_tree(Q, K, V, cu, 4, 3, Kp=Kp, Vp=Vp)
+    check_bf16(O.double().cpu().numpy(), o_ref, "bf16 prefix")
+    assert np.abs(LSE.double().cpu().numpy() - lse_ref).max() <= 2e-3
+
+
+def test_prefix_equals_merge_pipeline():
+    """The fused path equals the reference's three-step pipeline:
+    prefix attention with LSE, tree attention with LSE, fused_lse_merge."""
+    ra = _ra()
+    B, b, d, H, D, L = 2, 4, 3, 8, 128, 640
+    N = num_tree_nodes(b, d)
+    Q, K, V, cu = tree_case(B, b, d, H, D)
+    Kp, Vp = _prefix(B, L, H, D, 12)
+    Qd, Kd, Vd = Q.to(DEV), K.to(DEV), V.to(DEV)
+    fused = ra.ragged_attention_prefix(Qd, Kd, Vd, cu, Kp.to(DEV), Vp.to(DEV), b, d)
+    # step 1: prefix-only attention (a tree walk of depth 0 would add the self
+    # key, so use the oracle's prefix-only state through the merge identity)
+    anc_none = np.full((B * N, 1), -1, dtype=np.int32)
+    o_p, lse_p = clib.tree_attn(Q.float().numpy(), K.float().numpy(), V.float().numpy(), cu.numpy(), anc_none,
+                                1 / np.sqrt(D), Kp.float().numpy(), Vp.float().numpy())
+    o_t, lse_t = ra.ragged_attention_with_lse(Qd, Kd, Vd, cu, b, d)
+    to_bhn = lambda x: x.view(B, N, H, -1).permute(0, 2, 1, 3)
+    merged = ra.fused_lse_merge(
+        torch.from_numpy(lse_p).float().view(B, N, H).permute(0, 2, 1).to(DEV),
+        lse_t.view(B, N, H).permute(0, 2, 1),
+        to_bhn(torch.from_numpy(o_p).half().to(DEV)), to_bhn(o_t))
+    merged = merged.permute(0, 2, 1, 3).reshape(B * N, H, D)
+    assert (fused.float() - merged.float()).abs().max().item() <= 4e-3
+
+
+# ---------------------------------------------------------------------------
+# full-size BASELINE prefix configurations
+# ---------------------------------------------------------------------------
+
+def test_cfg4_full_size():
+    """B=4, L=10240 per sequence, b=4 d=3 (N=85), Hq=32, Hkv=8, D=128: checked
+    against the fp32 padded-SDPA oracle (MATH) on the CPU."""
+    ra = _ra()
+    B, b, d, Hq, Hkv, D, L = 4, 4, 3, 32, 8, 128, 10240
+    N = num_tree_nodes(b, d)
+    say("cfg4 full size")
+    Q, K, V, cu = tree_case(B, b, d, Hq, D, Hkv=Hkv)
+    Kp, Vp = _prefix(B, L, Hkv, D, B * 10000 + b * 100 + d + 1)
+    O = ra.ragged_attention_prefix(Q.to(DEV), K.to(DEV), V.to(DEV), cu, Kp.to(DEV), Vp.to(DEV), b, d)
+    from oracle import tree as otree
+    masks = [otree.tree_attention_mask(b, d)] * B
+    ref = sdpa.packed_tree_attention(Q, K, V, cu, masks, Kp=Kp, Vp=Vp)
+    check_fp16(O.double().cpu().numpy(), ref.double().numpy(), "cfg4")
+
+
+def test_cfg5_sampled():
+    """B=16, L=2048, b=8 d=4 (N=4681), H=32, sigma=0.5: the GPU runs the full
+    configuration; the oracle checks sequences 0 and 15 on 4 heads each."""
+    ra = _ra()
+    B, b, d, H, D, L = 16, 8, 4, 32, 128, 2048
+    N = num_tree_nodes(b, d)
+    say("cfg5 full size")
+    Q, K, V, cu = make_inputs([N] * B, H, D, B * 10000 + b * 100 + d, sigma=0.5)
+    Kp, Vp = _prefix(B, L, H, D, B * 10000 + b * 100 + d + 1, sigma=0.5)
+    O = ra.ragged_attention_prefix(Q.to(DEV), K.to(DEV), V.to(DEV), cu, Kp.to(DEV), Vp.to(DEV), b, d)
+    O = O.cpu()
+    assert torch.isfinite(O.float()).all()
+    from oracle import tree as otree
+    m = otree.tree_attention_mask(b, d)
+    for s in (0, 15):
+        rows = slice(s * N, (s + 1) * N)
+        heads = slice(4 * (s % 8), 4 * (s % 8) + 4)
+        ref = sdpa.padded_sdpa([Q[rows, heads]], [K[rows, heads]], [V[rows, heads]], [m],
+                               [Kp[s, :, heads]], [Vp[s, :, heads]])[0][0]
+        check_fp16(O[rows, heads].double().numpy(), ref.double().numpy(), f"cfg5 seq {s}")

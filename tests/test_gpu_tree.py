@@ -154,15 +154,19 @@ def test_single_token_and_chain(b, d):
         assert np.array_equal(o, V.double().numpy())
 
 
-def test_gather_and_subtree_bitexact():
-    """Both kernels fold the same steps in the same order with the same
-    arithmetic, so their outputs agree bit for bit."""
+def test_gather_and_subtree_agree():
+    """The two kernels differ only in fp32 summation order, so their fp16
+    outputs agree to one ulp and their LSEs to fp32 rounding."""
     for (B, b, d, H, D) in [(4, 4, 5, 8, 128), (2, 2, 7, 4, 64), (3, 3, 4, 4, 32), (2, 1, 40, 2, 64)]:
-        say("gather==subtree", B, b, d)
+        say("gather~subtree", B, b, d)
         Q, K, V, cu = tree_case(B, b, d, H, D)
         o1, l1 = run_tree(Q, K, V, cu, b, d, algo=1)
         o2, l2 = run_tree(Q, K, V, cu, b, d, algo=2)
-        assert np.array_equal(o1, o2) and np.array_equal(l1, l2)
+        # two fp16 roundings of values that differ by fp32 noise: <= 2 ulp
+        ulp = 2.0 ** (np.floor(np.log2(np.maximum(np.abs(o1), 2.0 ** -14))) - 10)
+        bad = np.abs(o1 - o2) > 2 * ulp
+        assert not bad.any(), f"{bad.sum()} elements differ by more than 2 ulp"
+        assert np.abs(l1 - l2).max() <= 1e-5
 
 
 # ---------------------------------------------------------------------------
