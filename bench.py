@@ -1,19 +1,23 @@
 """Benchmark of the tree-verify attention hot path on one MI355X.
 
-    python bench.py [--steps K] [--warmup W] [--config cfg2|cfg3] [--algo auto|gather|subtree]
+    python bench.py [--steps K] [--warmup W] [--config cfg2|cfg3|cfg4|cfg5] [--algo auto|gather|subtree]
 
-A step is one full verify-attention call (all sequences, all heads) over one
-batch of synthetic input, exactly what the reference times per call
-(scripts/benchmark_micro.py:585-609).  Inputs are generated on the CPU with
-the reference seed convention, copied to HBM before timing, and rotated over
-several independent sets whose total exceeds 512 MB, so that MI355X's 256 MB
-Infinity Cache cannot serve a call from the previous call's data.  Each set's
-call is captured in a HIP graph (the reference times CUDA-graph replays,
-scripts/benchmark_micro.py:169-187); the timed region replays K graphs,
+A step is one full verify-attention call (all sequences, all heads, and the
+prefix KV cache when the config has one) over one batch of synthetic input,
+what the reference times per call (scripts/benchmark_micro.py:585-609).
+Inputs are drawn on the CPU with the reference seed convention
+(B*10000 + b*100 + d), copied to HBM before timing, and rotated over several
+independent sets whose total exceeds 512 MB, so MI355X's 256 MB Infinity
+Cache cannot serve a call from the previous call's data.  The calls are
+captured in HIP graphs (the reference times CUDA-graph replays,
+scripts/benchmark_micro.py:169-187), 8 calls per graph so graph-launch gaps do
+not pad the per-call time; the timed region replays graphs for exactly K calls,
 bracketed by torch.cuda.synchronize().
 
 Prints ONE JSON line with the driver's fields plus
-  roofline      algorithmic bytes / measured kernel time vs 8 TB/s HBM
+  roofline      tree-only configs: algorithmic bytes (Q+K+V+O) / kernel time
+                vs 8 TB/s HBM.  Prefix configs: t_min = max(bytes / 8 TB/s,
+                flops / 2.5 PFLOP/s) and frac = t_min / t.
   cpu_baseline  the reference's CPU path (padded SDPA + tree mask, fp32, MATH
                 backend; restated in oracle/sdpa.py) timed on this host's cores
 """
@@ -21,7 +25,6 @@ from __future__ import annotations
 
 import argparse
 import json
-import math
 import os
 import sys
 import time
@@ -30,12 +33,16 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 METRIC = "verify-attn µs/call + achieved HBM GB/s, b=4 d=5 N=1365 H=32 D=128 fp16"
-PEAK_HBM = 8.0e12  # B/s, MI355X HBM3E (vendor figure)
+PEAK_HBM = 8.0e12     # B/s, MI355X HBM3E (vendor figure)
+PEAK_MFMA = 2.5e15    # FLOP/s, MI355X dense fp16 MFMA (vendor figure)
+CALLS_PER_GRAPH = 8
 
+# BASELINE.json configs[1..4]
 CONFIGS = {
-    # name: (B, b, d, H, D) -- BASELINE.json configs[1] and [2]
-    "cfg2": (4, 4, 5, 32, 128),
-    "cfg3": (8, 2, 9, 32, 128),
+    "cfg2": dict(B=4, b=4, d=5, H=32, Hkv=32, D=128, L=0, sigma=1.0),
+    "cfg3": dict(B=8, b=2, d=9, H=32, Hkv=32, D=128, L=0, sigma=1.0),
+    "cfg4": dict(B=4, b=4, d=3, H=32, Hkv=8, D=128, L=10240, sigma=1.0),
+    "cfg5": dict(B=16, b=8, d=4, H=32, Hkv=32, D=128, L=2048, sigma=0.5),
 }
 
 
@@ -43,41 +50,70 @@ def num_tree_nodes(b, d):
     return d + 1 if b == 1 else (b ** (d + 1) - 1) // (b - 1)
 
 
-def make_set(B, b, d, H, D, seed, dtype):
+def make_set(c, seed, dtype):
+    """Q, tree K, tree V (packed) and prefix K/V [B, L, Hkv, D], drawn in that order."""
     import torch
+    N = num_tree_nodes(c["b"], c["d"])
+    T = c["B"] * N
+    g = torch.Generator().manual_seed(seed)
+    s = c["sigma"]
+    Q = (torch.randn(T, c["H"], c["D"], generator=g) * s).to(dtype)
+    K = (torch.randn(T, c["Hkv"], c["D"], generator=g) * s).to(dtype)
+    V = (torch.randn(T, c["Hkv"], c["D"], generator=g) * s).to(dtype)
+    Kp = Vp = None
+    if c["L"]:
+        Kp = (torch.randn(c["B"], c["L"], c["Hkv"], c["D"], generator=g) * s).to(dtype)
+        Vp = (torch.randn(c["B"], c["L"], c["Hkv"], c["D"], generator=g) * s).to(dtype)
+    return Q, K, V, Kp, Vp
+
+
+def model_costs(c):
+    """Algorithmic HBM bytes and FLOPs of one call."""
+    B, b, d, H, Hkv, D, L = (c[k] for k in ("B", "b", "d", "H", "Hkv", "D", "L"))
     N = num_tree_nodes(b, d)
     T = B * N
-    g = torch.Generator().manual_seed(seed)
-    Q = torch.randn(T, H, D, generator=g).to(dtype)
-    K = torch.randn(T, H, D, generator=g).to(dtype)
-    V = torch.randn(T, H, D, generator=g).to(dtype)
-    return Q, K, V
+    tree_bytes = 2 * T * D * (2 * H + 2 * Hkv)          # Q + O at H, tree K + V at Hkv
+    prefix_bytes = 2 * 2 * B * L * Hkv * D                 # prefix K + V at Hkv
+    steps = sum((b ** k) * (k + 1) for k in range(d + 1)) if b > 1 else sum(k + 1 for k in range(d + 1))
+    tree_flops = 4 * D * H * B * steps
+    prefix_flops = 4 * B * N * H * L * D
+    return tree_bytes + prefix_bytes, tree_flops + prefix_flops, prefix_flops
 
 
-def cpu_baseline(B, b, d, H, D, budget_s=20.0):
-    """Reference CPU path on a bounded sample: padded SDPA (fp32, MATH) with the
-    tree mask over the full configuration, repeated until ~budget_s."""
+def cpu_baseline(c, budget_s=20.0):
+    """Reference CPU path on a bounded sample: padded SDPA (fp32, MATH) with
+    the tree mask (prefix columns all-attend), repeated until ~budget_s."""
     import numpy as np
     import torch
     from oracle import sdpa, tree
 
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
+    B, b, d = c["B"], c["b"], c["d"]
     N = num_tree_nodes(b, d)
-    Q, K, V = make_set(B, b, d, H, D, B * 10000 + b * 100 + d, torch.float16)
-    Q, K, V = Q.float(), K.float(), V.float()
-    cu = torch.arange(0, (B + 1) * N, N, dtype=torch.int32)
-    masks = [tree.tree_attention_mask_n(b, N)] * B
+    Q, K, V, Kp, Vp = make_set(c, B * 10000 + b * 100 + d, torch.float16)
+    nseq = B
+    if c["L"] and B * N * (N + c["L"]) * c["H"] > 4e9:
+        nseq = 1  # sample: one sequence of the batch (the full score tensor would not fit)
+    Q, K, V = (t[:nseq * N].float() for t in (Q, K, V))
+    Kp = Kp[:nseq].float() if Kp is not None else None
+    Vp = Vp[:nseq].float() if Vp is not None else None
+    cu = torch.arange(0, (nseq + 1) * N, N, dtype=torch.int32)
+    masks = [tree.tree_attention_mask_n(b, N)] * nseq
+
+    def run():
+        sdpa.packed_tree_attention(Q, K, V, cu, masks, Kp=Kp, Vp=Vp)
+
     t0 = time.perf_counter()
-    sdpa.packed_tree_attention(Q, K, V, cu, masks)  # warmup
+    run()  # warmup
     first = time.perf_counter() - t0
     iters = max(1, min(20, int(budget_s / max(first, 1e-3))))
     times = []
     for _ in range(iters):
         t0 = time.perf_counter()
-        sdpa.packed_tree_attention(Q, K, V, cu, masks)
+        run()
         times.append(time.perf_counter() - t0)
-    med = float(np.median(times))
+    med = float(np.median(times)) * (B / nseq)
     model = ""
     try:
         for line in open("/proc/cpuinfo"):
@@ -86,13 +122,15 @@ def cpu_baseline(B, b, d, H, D, budget_s=20.0):
                 break
     except OSError:
         pass
+    what = f"{nseq} of {B} sequences, scaled x{B // nseq} to the full batch" if nseq < B else "the full config"
     return {
         "value": round(med * 1e6, 1),
         "unit": "us/call",
         "cores": cores,
         "kind": "port",
-        "sample": (f"full config B={B} b={b} d={d} N={N} H={H} D={D}: padded SDPA fp32 MATH with the "
-                   f"ancestor mask (oracle/sdpa.py), median of {iters} calls after 1 warmup; CPU {model}"),
+        "sample": (f"{what} (B={B} b={b} d={d} N={N} H={c['H']} Hkv={c['Hkv']} D={c['D']} L={c['L']}): "
+                   f"padded SDPA fp32 MATH with the ancestor mask (oracle/sdpa.py), median of {iters} calls "
+                   f"after 1 warmup; CPU {model}"),
     }
 
 
@@ -100,59 +138,67 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--config", default="cfg2", choices=sorted(CONFIGS))
     ap.add_argument("--algo", default="auto", choices=["auto", "gather", "subtree"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--sets", type=int, default=4, help="rotating input sets (cache flush)")
+    ap.add_argument("--sets", type=int, default=0, help="rotating input sets (0: enough for > 512 MB)")
     args = ap.parse_args()
 
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
-              "the tree path shards over sequences/heads with no exchange, see DESIGN.md", file=sys.stderr)
+              "the tree path shards over sequences/heads with no exchange (see DESIGN.md)", file=sys.stderr)
         sys.exit(2)
 
     import torch
     from qattention_amd import _lib
     from qattention_amd import ragged_attn as ra
 
-    B, b, d, H, D = CONFIGS[args.config]
+    c = CONFIGS[args.config]
+    B, b, d, H, Hkv, D, L = (c[k] for k in ("B", "b", "d", "H", "Hkv", "D", "L"))
     N = num_tree_nodes(b, d)
     T = B * N
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     algo = {"auto": _lib.ALGO_AUTO, "gather": _lib.ALGO_GATHER, "subtree": _lib.ALGO_SUBTREE}[args.algo]
+    alg_bytes, flops, prefix_flops = model_costs(c)
+    nsets = args.sets or max(2, min(8, -(-600_000_000 // alg_bytes)))
 
     seed = B * 10000 + b * 100 + d
     sets = []
-    for i in range(args.sets):
-        Q, K, V = make_set(B, b, d, H, D, seed + i, torch.float16)
-        sets.append((Q.to(dev), K.to(dev), V.to(dev)))
+    for i in range(nsets):
+        sets.append([t.to(dev) if t is not None else None for t in make_set(c, seed + i, torch.float16)])
     cu = torch.arange(0, (B + 1) * N, N, dtype=torch.int32, device=dev)
     torch.cuda.synchronize()
 
     def call(i):
-        Q, K, V = sets[i]
+        Q, K, V, Kp, Vp = sets[i]
+        if L:
+            return ra.ragged_attention_prefix(Q, K, V, cu, Kp, Vp, b, d, max_seqlen=N)
         return ra._tree_forward(Q, K, V, cu, b, d, N, False, algo)[0]
 
-    # warm up eagerly, then capture one graph per input set
-    for i in range(len(sets)):
+    for i in range(nsets):
         call(i)
     torch.cuda.synchronize()
-    graphs, outs = [], []
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
-        for i in range(len(sets)):
+        for i in range(nsets):
             call(i)
     torch.cuda.current_stream().wait_stream(side)
-    for i in range(len(sets)):
+    torch.cuda.synchronize()
+    # one graph per input set, CALLS_PER_GRAPH calls each
+    graphs = []
+    for i in range(nsets):
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
-            outs.append(call(i))
+            for _ in range(CALLS_PER_GRAPH):
+                call(i)
         graphs.append(g)
-    for k in range(args.warmup):
-        graphs[k % len(graphs)].replay()
+    replays = max(1, -(-args.steps // CALLS_PER_GRAPH))
+    steps = replays * CALLS_PER_GRAPH
+    for k in range(max(1, args.warmup // CALLS_PER_GRAPH)):
+        graphs[k % nsets].replay()
     torch.cuda.synchronize()
 
     stream = torch.cuda.current_stream()
@@ -160,51 +206,61 @@ def main():
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     ev0.record(stream)
-    for k in range(args.steps):
-        graphs[k % len(graphs)].replay()
+    for k in range(replays):
+        graphs[k % nsets].replay()
     ev1.record(stream)
     torch.cuda.synchronize()
     t1 = time.perf_counter()
-    wall_us = (t1 - t0) / args.steps * 1e6
-    event_us = ev0.elapsed_time(ev1) * 1e3 / args.steps
+    wall_us = (t1 - t0) / steps * 1e6
+    event_us = ev0.elapsed_time(ev1) * 1e3 / steps
 
-    alg_bytes = 4 * T * H * D * 2  # Q + K + V + O, fp16
-    achieved = alg_bytes / (event_us * 1e-6)
-    flops = 4 * D * H * B * sum((b ** k) * (k + 1) for k in range(d + 1)) if b > 1 else 0
-
+    t_s = event_us * 1e-6
+    achieved_bw = alg_bytes / t_s
+    if L:
+        t_min = max(alg_bytes / PEAK_HBM, flops / PEAK_MFMA)
+        bound = "mfma" if flops / PEAK_MFMA >= alg_bytes / PEAK_HBM else "hbm"
+        roofline = {"bound": bound, "achieved": round(flops / t_s / 1e12, 1) if bound == "mfma"
+                    else round(achieved_bw / 1e9, 1),
+                    "peak": PEAK_MFMA / 1e12 if bound == "mfma" else PEAK_HBM / 1e9,
+                    "unit": "TFLOP/s" if bound == "mfma" else "GB/s",
+                    "frac": round(t_min / t_s, 4), "t_min_us": round(t_min * 1e6, 2),
+                    "hbm_frac": round(achieved_bw / PEAK_HBM, 4),
+                    "mfma_frac": round(flops / t_s / PEAK_MFMA, 4)}
+    else:
+        roofline = {"bound": "hbm", "achieved": round(achieved_bw / 1e9, 1), "peak": PEAK_HBM / 1e9,
+                    "unit": "GB/s", "frac": round(achieved_bw / PEAK_HBM, 4)}
     traffic = None
-    prof = os.path.join(ROOT, "profiles", f"tree_{args.config}_traffic.json")
+    prof = os.path.join(ROOT, "profiles", f"traffic_{args.config}.json")
     if os.path.exists(prof):
         try:
             traffic = json.load(open(prof)).get("hbm_bytes_per_dispatch")
         except (OSError, ValueError):
             traffic = None
+    roofline.update({"traffic": traffic, "algorithmic_bytes": alg_bytes, "flops": flops})
 
     cpu = None
     if not args.no_cpu_baseline:
-        cpu = cpu_baseline(B, b, d, H, D)
+        cpu = cpu_baseline(c)
 
     out = {
         "metric": METRIC,
         "value": round(event_us, 2),
         "unit": "us/call",
         "n_gpus": 1,
-        "steps": args.steps,
+        "steps": steps,
         "warmup": args.warmup,
         "ms_per_step": round(wall_us / 1e3, 5),
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f16",
-        "data": "synthetic N(0,1), CPU-seeded (seed B*10000+b*100+d), 4 rotating sets > 512 MB",
-        "config": {"workload": f"{args.config}: tree-only verify attention B={B} b={b} d={d} N={N} "
-                               f"H={H} D={D} fp16", "B": B, "b": b, "d": d, "N": N, "H": H, "D": D,
-                   "tokens": T, "algo": args.algo},
-        "achieved_GBps": round(achieved / 1e9, 1),
+        "data": f"synthetic N(0,{c['sigma']}^2), CPU-seeded (seed B*10000+b*100+d), {nsets} rotating sets",
+        "config": {"workload": f"{args.config}: verify attention B={B} b={b} d={d} N={N} H={H} Hkv={Hkv} "
+                               f"D={D} L={L} fp16", "B": B, "b": b, "d": d, "N": N, "H": H, "Hkv": Hkv,
+                   "D": D, "L": L, "tokens": T, "algo": args.algo},
+        "achieved_GBps": round(achieved_bw / 1e9, 1),
         "wall_us_per_call": round(wall_us, 2),
-        "roofline": {"bound": "hbm", "achieved": round(achieved / 1e9, 1), "peak": PEAK_HBM / 1e9,
-                     "unit": "GB/s", "frac": round(achieved / PEAK_HBM, 4), "traffic": traffic,
-                     "algorithmic_bytes": alg_bytes, "flops": flops},
+        "roofline": roofline,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

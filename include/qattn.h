@@ -24,7 +24,8 @@
  *     max_seqlen bounds every sequence length (tokens at or beyond it are not
  *     computed).  A sequence whose offsets are decreasing, negative or beyond
  *     total_tokens is skipped (its output rows are left untouched).
- *   - scale multiplies q.k (the reference fixes it to 1/sqrt(head_dim)).
+ *   - scale multiplies q.k (the reference fixes it to 1/sqrt(head_dim));
+ *     qattn_prefix_tree_fwd requires scale > 0.
  *   - lse (optional, may be NULL) is fp32 [tokens, num_q_heads] with strides
  *     {stride_token, stride_head}: lse = m + ln(sum exp(s - m)).
  */

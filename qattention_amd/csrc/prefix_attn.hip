@@ -1,30 +1,39 @@
 // prefix_attn.hip -- MFMA flash attention of tree-verify queries over a prefix
-// KV cache (the dense half of src/ragged_attn.py:1761-1798), split along the
-// prefix (flash-decoding) and merged into the tree walk's softmax state.
+// KV cache (the dense half of src/ragged_attn.py:1761-1798), merged into the
+// ancestor walk's softmax state.
 //
-// Work unit: (sequence, kv head, query tile of 64 rows, prefix split).  The 64
+// Work unit: (sequence, kv head, query tile of 128 rows, prefix split).  The
 // rows of a tile are (token, q head) pairs of ONE kv head's GQA group, so a
 // K/V block staged in LDS serves every q head that reads it (no repeat_kv).
-// Each of the 4 waves owns 16 rows and computes, per 64-key block,
-//   S^T = K Q^T            16 x v_mfma_f32_16x16x32_{f16,bf16}
-//   O^T += V^T P^T         16 x v_mfma_f32_16x16x32_{f16,bf16}   (D = 128)
-// Computing S transposed puts one query per lane column, so the softmax row
-// statistics need only a 4-lane (xor 16, xor 32) reduction and the MFMA
-// output of S^T is directly the B operand P^T of the next product (keys are
-// permuted consistently in P^T and in the LDS copy of V^T).
-// The split's unnormalised state (m, l, acc) is written to a caller-provided
-// workspace; the tree kernels (tree_attn.hip) merge all splits, walk the
-// ancestors and normalise.
+// Each of the 4 waves owns 32 rows as two 16-column blocks and computes, per
+// 64-key block,
+//   S^T = K Q^T      32 x v_mfma_f32_16x16x32_{f16,bf16}   (D = 128)
+//   O^T += V^T P^T   32 x v_mfma_f32_16x16x32_{f16,bf16}
+// Every K and V^T operand read from LDS feeds both column blocks.  Computing
+// S transposed puts one query per lane column, so the softmax statistics need
+// only a 4-lane (xor 16, xor 32) reduction, and the S^T output registers are
+// directly the P^T operand of the next product (keys are permuted the same way
+// in P^T and in the LDS copy of V^T).
+//
+// Two ways to finish:
+//  * several prefix splits: each split writes its unnormalised state
+//    (m, l, acc) to a caller workspace and the tree kernels (tree_attn.hip)
+//    merge the splits, walk the ancestors and normalise;
+//  * one split (enough query tiles to fill the GPU): the epilogue hands the
+//    state to the ancestor walk in the same workgroup (gather_walk4), which
+//    normalises and stores O -- no partial state leaves the chip.
 #include <algorithm>
 
 #include "qattn_common.h"
 #include "qattn_device.h"
+#include "tree_walk.h"
 
 namespace qattn {
 
 constexpr int kPrefixThreads = 256;
-constexpr int kBN = 64;  // prefix keys per block
-constexpr int kBM = 64;  // query rows per workgroup (4 waves x 16)
+constexpr int kBN = 64;   // prefix keys per block
+constexpr int kQB = 2;    // 16-row column blocks per wave
+constexpr int kBM = 4 * 16 * kQB;  // query rows per workgroup
 
 struct PrefixParams {
     const void* q;
@@ -85,15 +94,18 @@ __device__ __forceinline__ int vt_col(int k) {
     return 32 * half + 8 * g + 4 * u + j;
 }
 
-template <typename T, int D>
-__global__ __launch_bounds__(kPrefixThreads) void prefix_splitk_kernel(PrefixParams p) {
+template <typename T, int D, bool FUSED, bool LSE>
+__global__ __launch_bounds__(kPrefixThreads) __attribute__((amdgpu_waves_per_eu(1, 2))) void prefix_attn_kernel(
+    PrefixParams p, TreeParams tp) {
     constexpr int NC = D / 32;      // MFMA k-chunks over the head dim
     constexpr int ND = D / 16;      // output tiles over the head dim
     constexpr int KROW = D + 8;     // Ks row stride in elements (16-byte pad)
     constexpr int VROW = kBN + 8;   // Vt row stride in elements
     constexpr int DV = D / 8;       // 16-byte vectors per head row
-    __shared__ __attribute__((aligned(16))) uint16_t Ks[kBN * KROW];
-    __shared__ __attribute__((aligned(16))) uint16_t Vt[D * VROW];
+    constexpr int LDS_HALVES = kBN * KROW + D * VROW;
+    __shared__ __attribute__((aligned(16))) uint16_t lds[LDS_HALVES];
+    uint16_t* Ks = lds;
+    uint16_t* Vt = lds + kBN * KROW;
 
     // Logical unit order puts the query tiles of one (sequence, kv head, split)
     // next to each other; hardware deals blockIdx round-robin over the 8 XCDs,
@@ -117,23 +129,29 @@ __global__ __launch_bounds__(kPrefixThreads) void prefix_splitk_kernel(PrefixPar
     if (qt * kBM >= rows) return;
 
     const int tid = threadIdx.x;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lane = tid & 63;
     const int l16 = lane & 15;
     const int lq = lane >> 4;
 
-    // this lane's query row (B operand column / output column)
-    const int rr = qt * kBM + wave * 16 + l16;
-    const bool rvalid = rr < rows;
-    const int tok = rvalid ? divide(rr, p.gdiv) : 0;
-    const int qh = kvh * g + (rr - divide(rr, p.gdiv) * g);
-    const int64_t qrow = (int64_t)s0 + tok;
-
-    Vec16 qf[NC];
+    // this lane's query rows (B operand column / output column), one per block
+    int64_t qrow[kQB];
+    int qh[kQB];
+    bool rvalid[kQB];
+    Vec16 qf[kQB][NC];
 #pragma unroll
-    for (int c = 0; c < NC; ++c) {
-        qf[c] = Vec16{{0u, 0u, 0u, 0u}};
-        if (rvalid) qf[c] = ld16((const uint16_t*)p.q + qrow * p.sq_t + (int64_t)qh * p.sq_h + 32 * c + 8 * lq);
+    for (int b = 0; b < kQB; ++b) {
+        const int rr = qt * kBM + wave * (16 * kQB) + 16 * b + l16;
+        rvalid[b] = rr < rows;
+        const int tok = rvalid[b] ? divide(rr, p.gdiv) : 0;
+        qh[b] = kvh * g + (rr - divide(rr, p.gdiv) * g);
+        qrow[b] = (int64_t)s0 + tok;
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            qf[b][c] = Vec16{{0u, 0u, 0u, 0u}};
+            if (rvalid[b])
+                qf[b][c] = ld16((const uint16_t*)p.q + qrow[b] * p.sq_t + (int64_t)qh[b] * p.sq_h + 32 * c + 8 * lq);
+        }
     }
 
     const int k_lo = split * p.blocks_per_split * kBN;
@@ -141,31 +159,56 @@ __global__ __launch_bounds__(kPrefixThreads) void prefix_splitk_kernel(PrefixPar
     const uint16_t* kbase = (const uint16_t*)p.kp + (int64_t)seq * p.skp_b + (int64_t)kvh * p.skp_h;
     const uint16_t* vbase = (const uint16_t*)p.vp + (int64_t)seq * p.svp_b + (int64_t)kvh * p.svp_h;
 
-    float m_run = -INFINITY, l_run = 0.f;
-    f4_t oacc[ND];
+    float m_run[kQB], l_run[kQB];
+    f4_t oacc[kQB][ND];
 #pragma unroll
-    for (int i = 0; i < ND; ++i) oacc[i] = f4_t{0.f, 0.f, 0.f, 0.f};
+    for (int b = 0; b < kQB; ++b) {
+        m_run[b] = -INFINITY;
+        l_run[b] = 0.f;
+#pragma unroll
+        for (int i = 0; i < ND; ++i) oacc[b][i] = f4_t{0.f, 0.f, 0.f, 0.f};
+    }
 
-    for (int kb = k_lo; kb < k_hi; kb += kBN) {
-        // ---- stage K (row-major, padded) and V^T (column-permuted) in LDS ----
+    // ---- K/V block staging, software-pipelined through registers: the loads
+    // of block i+1 are issued right after block i is in LDS and land while the
+    // MFMAs of block i run ----
+    constexpr int KU = kBN * DV / kPrefixThreads;                        // K vectors per thread
+    constexpr int VUNITS = (kBN / 4) * DV;                                // 4-key x 8-dim V units
+    constexpr int VU = (VUNITS + kPrefixThreads - 1) / kPrefixThreads;   // V units per thread
+    Vec16 kreg[KU], vreg[VU][4];
+    auto load_block = [&](int kb) {
 #pragma unroll
-        for (int u = tid; u < kBN * DV; u += kPrefixThreads) {
+        for (int i = 0; i < KU; ++i) {
+            const int u = tid + i * kPrefixThreads;
             const int key = u / DV, ch = u % DV;
-            Vec16 x = Vec16{{0u, 0u, 0u, 0u}};
-            if (kb + key < k_hi) x = ld16(kbase + (int64_t)(kb + key) * p.skp_t + 8 * ch);
-            st16(Ks + key * KROW + 8 * ch, x);
+            kreg[i] = Vec16{{0u, 0u, 0u, 0u}};
+            if (kb + key < k_hi) kreg[i] = ld16(kbase + (int64_t)(kb + key) * p.skp_t + 8 * ch);
         }
 #pragma unroll
-        for (int u = tid; u < (kBN / 4) * DV; u += kPrefixThreads) {
+        for (int i = 0; i < VU; ++i) {
+            const int u = tid + i * kPrefixThreads;
             const int kg = u % (kBN / 4), dch = u / (kBN / 4);
-            Vec16 v4[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int key = kb + 4 * kg + i;
-                v4[i] = Vec16{{0u, 0u, 0u, 0u}};
-                if (key < k_hi) v4[i] = ld16(vbase + (int64_t)key * p.svp_t + 8 * dch);
+            for (int rk = 0; rk < 4; ++rk) {
+                const int key = kb + 4 * kg + rk;
+                vreg[i][rk] = Vec16{{0u, 0u, 0u, 0u}};
+                if (u < VUNITS && key < k_hi) vreg[i][rk] = ld16(vbase + (int64_t)key * p.svp_t + 8 * dch);
             }
+        }
+    };
+    auto store_block = [&]() {
+#pragma unroll
+        for (int i = 0; i < KU; ++i) {
+            const int u = tid + i * kPrefixThreads;
+            st16(Ks + (u / DV) * KROW + 8 * (u % DV), kreg[i]);
+        }
+#pragma unroll
+        for (int i = 0; i < VU; ++i) {
+            const int u = tid + i * kPrefixThreads;
+            if (u >= VUNITS) continue;
+            const int kg = u % (kBN / 4), dch = u / (kBN / 4);
             const int col = vt_col(4 * kg);
+            const Vec16* v4 = vreg[i];
 #pragma unroll
             for (int m = 0; m < 4; ++m) {
                 // d = 8 dch + 2m (low halves) and 8 dch + 2m + 1 (high halves)
@@ -177,95 +220,204 @@ __global__ __launch_bounds__(kPrefixThreads) void prefix_splitk_kernel(PrefixPar
                 *reinterpret_cast<uint2*>(Vt + (8 * dch + 2 * m + 1) * VROW + col) = make_uint2(o01, o23);
             }
         }
-        __syncthreads();
+    };
 
+    if (k_lo < k_hi) load_block(k_lo);
+    // One 64-key block from LDS; MASK instantiates the split's tail block, the
+    // only one with keys beyond k_hi, so full blocks carry no masking code.
+    auto compute_block = [&](int kb, auto mask_tag) {
+        constexpr bool MASK = decltype(mask_tag)::value;
         // ---- S^T = K Q^T: lane holds keys 16 mt + 4 lq + i of query l16 ----
-        f4_t sacc[4];
+        f4_t sacc[kQB][4];
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt) {
-            sacc[mt] = f4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int b = 0; b < kQB; ++b) sacc[b][mt] = f4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int c = 0; c < NC; ++c) {
                 const Vec16 a = ld16(Ks + (16 * mt + l16) * KROW + 32 * c + 8 * lq);
-                sacc[mt] = MfmaOps<T>::mma(a, qf[c], sacc[mt]);
+#pragma unroll
+                for (int b = 0; b < kQB; ++b) sacc[b][mt] = MfmaOps<T>::mma(a, qf[b][c], sacc[b][mt]);
             }
         }
-        float s[4][4];
-        float mb = -INFINITY;
+        // ---- online softmax, per column block.  The running max is kept on
+        // raw scores q.k (scale > 0 keeps the order) and the scale*log2(e)
+        // factor is folded into the exponent: p = exp2(s c - m c), one FMA ----
+        const float c = p.scale_log2;
+        if constexpr (MASK) {  // tail block of the split: keys at or beyond k_hi do not exist
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
+            for (int b = 0; b < kQB; ++b)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int key = kb + 16 * mt + 4 * lq + i;
-                const float v = (key < k_hi) ? sacc[mt][i] * p.scale_log2 : -INFINITY;
-                s[mt][i] = v;
-                mb = fmaxf(mb, v);
+                for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        if (kb + 16 * mt + 4 * lq + i >= k_hi) sacc[b][mt][i] = -INFINITY;
+        }
+        // Lazy rescaling: the exponent reference m_run only moves when a block
+        // max exceeds it by more than kLazy/c (a factor 2^kLazy in P), so the
+        // accumulators are rescaled on a handful of blocks instead of nearly
+        // every block.  P stays <= 2^kLazy (exact in fp16/bf16 range, same
+        // relative precision) and l carries the same reference, so the final
+        // normalisation is unchanged.
+        constexpr float kLazy = 8.f;
+        Vec16 pf[kQB][2];
+        bool rescale = false;
+        float alpha[kQB];
+#pragma unroll
+        for (int b = 0; b < kQB; ++b) {
+            float mb = -INFINITY;
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) mb = fmaxf(mb, sacc[b][mt][i]);
+            mb = xor_max(mb, 16);
+            mb = xor_max(mb, 32);
+            const bool move = (mb - m_run[b]) * c > kLazy;  // always true on the first block
+            const float m_new = move ? mb : m_run[b];
+            alpha[b] = move ? fast_exp2((m_run[b] - m_new) * c) : 1.f;  // m_run = -inf: 0
+            rescale |= move;
+            const float mc = m_new * c;
+            float psum = 0.f;
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float e = fast_exp2(__builtin_fmaf(sacc[b][mt][i], c, -mc));
+                    sacc[b][mt][i] = e;
+                    psum += e;
+                }
+            }
+            l_run[b] = l_run[b] * alpha[b] + psum;
+            m_run[b] = m_new;
+#pragma unroll
+            for (int kc = 0; kc < 2; ++kc) {
+                pf[b][kc].w[0] = MfmaOps<T>::pack2(sacc[b][2 * kc][0], sacc[b][2 * kc][1]);
+                pf[b][kc].w[1] = MfmaOps<T>::pack2(sacc[b][2 * kc][2], sacc[b][2 * kc][3]);
+                pf[b][kc].w[2] = MfmaOps<T>::pack2(sacc[b][2 * kc + 1][0], sacc[b][2 * kc + 1][1]);
+                pf[b][kc].w[3] = MfmaOps<T>::pack2(sacc[b][2 * kc + 1][2], sacc[b][2 * kc + 1][3]);
             }
         }
-        mb = xor_max(mb, 16);
-        mb = xor_max(mb, 32);
-        const float m_new = fmaxf(m_run, mb);
-        const float alpha = fast_exp2(m_run - m_new);  // m_run = -inf on the first block: 0
-        float psum = 0.f;
+        // the accumulators need rescaling only when some running max moved
+        if (__builtin_expect(__any(rescale), 0)) {
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
+            for (int b = 0; b < kQB; ++b) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                s[mt][i] = fast_exp2(s[mt][i] - m_new);
-                psum += s[mt][i];
+                for (int dt = 0; dt < ND; ++dt) oacc[b][dt] *= alpha[b];
             }
         }
-        l_run = l_run * alpha + psum;
-        m_run = m_new;
-#pragma unroll
-        for (int dt = 0; dt < ND; ++dt) oacc[dt] *= alpha;
 
         // ---- O^T += V^T P^T, two 32-key chunks ----
-        Vec16 pf[2];
-#pragma unroll
-        for (int kc = 0; kc < 2; ++kc) {
-            pf[kc].w[0] = MfmaOps<T>::pack2(s[2 * kc][0], s[2 * kc][1]);
-            pf[kc].w[1] = MfmaOps<T>::pack2(s[2 * kc][2], s[2 * kc][3]);
-            pf[kc].w[2] = MfmaOps<T>::pack2(s[2 * kc + 1][0], s[2 * kc + 1][1]);
-            pf[kc].w[3] = MfmaOps<T>::pack2(s[2 * kc + 1][2], s[2 * kc + 1][3]);
-        }
 #pragma unroll
         for (int dt = 0; dt < ND; ++dt) {
 #pragma unroll
             for (int kc = 0; kc < 2; ++kc) {
                 const Vec16 a = ld16(Vt + (16 * dt + l16) * VROW + 32 * kc + 8 * lq);
-                oacc[dt] = MfmaOps<T>::mma(a, pf[kc], oacc[dt]);
+#pragma unroll
+                for (int b = 0; b < kQB; ++b) oacc[b][dt] = MfmaOps<T>::mma(a, pf[b][kc], oacc[b][dt]);
             }
         }
+    };
+
+    for (int kb = k_lo; kb < k_hi; kb += kBN) {
+        store_block();
+        __syncthreads();
+        if (kb + kBN < k_hi) load_block(kb + kBN);
+        if (kb + kBN <= k_hi)
+            compute_block(kb, std::false_type{});
+        else
+            compute_block(kb, std::true_type{});
         __syncthreads();
     }
 
-    // ---- partial state of this split: (m, l, unnormalised acc) ----
-    float l_tot = l_run + __shfl_xor(l_run, 16);
-    l_tot += __shfl_xor(l_tot, 32);
-    if (!rvalid) return;
-    const int64_t plane = p.total_tokens * (int64_t)p.Hq;
-    const int64_t idx = (int64_t)split * plane + qrow * p.Hq + qh;
-    if (lq == 0) {
-        p.part_m[idx] = m_run;
-        p.part_l[idx] = l_tot;
-    }
-    float* dst = p.part_acc + idx * D + 4 * lq;
+    float l_tot[kQB];
 #pragma unroll
-    for (int dt = 0; dt < ND; ++dt)
-        *reinterpret_cast<float4*>(dst + 16 * dt) = make_float4(oacc[dt][0], oacc[dt][1], oacc[dt][2], oacc[dt][3]);
+    for (int b = 0; b < kQB; ++b) {
+        l_tot[b] = l_run[b] + __shfl_xor(l_run[b], 16);
+        l_tot[b] += __shfl_xor(l_tot[b], 32);
+        m_run[b] *= p.scale_log2;  // to the log2 units of the tree walk's scores
+    }
+
+    if constexpr (!FUSED) {
+        // ---- partial state of this split: (m, l, unnormalised acc) ----
+        const int64_t plane = p.total_tokens * (int64_t)p.Hq;
+#pragma unroll
+        for (int b = 0; b < kQB; ++b) {
+            if (!rvalid[b]) continue;
+            const int64_t idx = (int64_t)split * plane + qrow[b] * p.Hq + qh[b];
+            if (lq == 0) {
+                p.part_m[idx] = m_run[b];
+                p.part_l[idx] = l_tot[b];
+            }
+            float* dst = p.part_acc + idx * D + 4 * lq;
+#pragma unroll
+            for (int dt = 0; dt < ND; ++dt)
+                *reinterpret_cast<float4*>(dst + 16 * dt) =
+                    make_float4(oacc[b][dt][0], oacc[b][dt][1], oacc[b][dt][2], oacc[b][dt][3]);
+        }
+    } else {
+        // ---- fused epilogue: re-lay each 16-row block in LDS as 4 lanes per
+        // query and run the ancestor walk from this state ----
+        constexpr int OROW = D + 4;  // fp32 row stride (pad)
+        float* Os = reinterpret_cast<float*>(lds) + wave * 16 * OROW;
+        float* Ms = reinterpret_cast<float*>(lds) + 4 * 16 * OROW + wave * 32;
+        static_assert((4 * 16 * OROW + 4 * 32) * 4 <= LDS_HALVES * 2, "epilogue staging must fit the LDS");
+        const int grp = lane >> 2, j = lane & 3;
+        constexpr int NCH = D / 32;
+#pragma unroll
+        for (int b = 0; b < kQB; ++b) {
+#pragma unroll
+            for (int dt = 0; dt < ND; ++dt)
+                *reinterpret_cast<float4*>(Os + l16 * OROW + 16 * dt + 4 * lq) =
+                    make_float4(oacc[b][dt][0], oacc[b][dt][1], oacc[b][dt][2], oacc[b][dt][3]);
+            if (lq == 0) {
+                Ms[l16] = m_run[b];
+                Ms[16 + l16] = l_tot[b];
+            }
+            __syncthreads();
+            const int rr = qt * kBM + wave * (16 * kQB) + 16 * b + grp;
+            if (rr < rows) {
+                const int tok = divide(rr, p.gdiv);
+                const int h = kvh * g + (rr - tok * g);
+                const int64_t qr = (int64_t)s0 + tok;
+                float acc[8 * NCH];
+#pragma unroll
+                for (int i = 0; i < NCH; ++i) {
+                    const float4 a0 = *reinterpret_cast<const float4*>(Os + grp * OROW + 8 * (j + 4 * i));
+                    const float4 a1 = *reinterpret_cast<const float4*>(Os + grp * OROW + 8 * (j + 4 * i) + 4);
+                    acc[8 * i + 0] = a0.x;
+                    acc[8 * i + 1] = a0.y;
+                    acc[8 * i + 2] = a0.z;
+                    acc[8 * i + 3] = a0.w;
+                    acc[8 * i + 4] = a1.x;
+                    acc[8 * i + 5] = a1.y;
+                    acc[8 * i + 6] = a1.z;
+                    acc[8 * i + 7] = a1.w;
+                }
+                float m = Ms[grp], l = Ms[16 + grp];
+                Vec16 qf4[NCH];
+                load_q4<D>(tp, qr, h, j, qf4);
+                gather_walk4<T, D, WALK_HEAP, KV_PACKED>(tp, seq, s0, n, tok, kvh, qf4, j, m, l, acc);
+                write_out4<T, D, LSE>(tp, qr, h, j, m, l, acc);
+            }
+            __syncthreads();
+        }
+    }
 }
 
 // ---------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------
-static int prefix_splits(int64_t units_per_split, int L, int num_splits, int& blocks_per_split) {
+static int64_t units_per_split(int batch, int hkv, int max_seqlen, int group) {
+    const int64_t qtiles = ((int64_t)max_seqlen * group + kBM - 1) / kBM;
+    return (int64_t)batch * hkv * qtiles;
+}
+
+// Split count along the prefix: enough work units for ~2 resident workgroups
+// on each of 256 CUs, never more splits than 64-key blocks.
+static int prefix_splits(int64_t ups, int L, int num_splits, int& blocks_per_split) {
     const int blocks = (L + kBN - 1) / kBN;
     int s = num_splits;
-    if (s <= 0) {
-        // aim for ~4 workgroups per CU on 256 CUs
-        s = (int)std::min<int64_t>(blocks, std::max<int64_t>(1, (1024 + units_per_split - 1) / units_per_split));
-    }
+    if (s <= 0) s = (int)std::max<int64_t>(1, (512 + ups / 2) / ups);
     s = std::max(1, std::min(s, std::max(blocks, 1)));
     blocks_per_split = (blocks + s - 1) / s;
     return blocks_per_split > 0 ? (blocks + blocks_per_split - 1) / blocks_per_split : 1;
@@ -274,24 +426,28 @@ static int prefix_splits(int64_t units_per_split, int L, int num_splits, int& bl
 static int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
 
 static int64_t workspace_bytes(int64_t total_tokens, int hq, int head_dim, int splits) {
+    if (splits <= 1) return 0;  // one split: fused epilogue, no partial states
     const int64_t plane = total_tokens * hq;
     return 2 * align256(splits * plane * 4) + align256(splits * plane * head_dim * 4);
 }
 
-static int64_t units_per_split(int batch, int hkv, int max_seqlen, int group) {
-    const int64_t qtiles = ((int64_t)max_seqlen * group + kBM - 1) / kBM;
-    return (int64_t)batch * hkv * qtiles;
-}
-
 template <typename T, int D>
-static int launch_prefix(const PrefixParams& pp, hipStream_t st) {
+static int launch_prefix(const PrefixParams& pp, const TreeParams& tp, bool fused, hipStream_t st) {
     const int64_t grid = ((int64_t)pp.n_units + 7) / 8 * 8;
     if (grid >= (int64_t(1) << 31)) {
         set_error("prefix grid too large");
         return QATTN_ERR_ARG;
     }
-    hipLaunchKernelGGL((prefix_splitk_kernel<T, D>), dim3((unsigned)grid), dim3(kPrefixThreads), 0, st, pp);
-    return launch_status("prefix_splitk_kernel");
+    if (!fused)
+        hipLaunchKernelGGL((prefix_attn_kernel<T, D, false, false>), dim3((unsigned)grid), dim3(kPrefixThreads), 0,
+                           st, pp, tp);
+    else if (tp.lse)
+        hipLaunchKernelGGL((prefix_attn_kernel<T, D, true, true>), dim3((unsigned)grid), dim3(kPrefixThreads), 0,
+                           st, pp, tp);
+    else
+        hipLaunchKernelGGL((prefix_attn_kernel<T, D, true, false>), dim3((unsigned)grid), dim3(kPrefixThreads), 0,
+                           st, pp, tp);
+    return launch_status("prefix_attn_kernel");
 }
 
 }  // namespace qattn
@@ -324,6 +480,10 @@ int qattn_prefix_tree_fwd(const void* q, const int64_t q_stride[3], const void* 
     clear_error();
     int rc = check_common(dtype, head_dim, batch, max_seqlen, total_tokens, num_q_heads, num_kv_heads, max_depth);
     if (rc) return rc;
+    if (!(scale > 0.f)) {
+        set_error("scale must be positive (got %g)", (double)scale);
+        return QATTN_ERR_ARG;
+    }
     if (prefix_len < 0 || tree_seq_stride < 0 || tree_row0 < 0) {
         set_error("bad prefix_len / tree layout (%d, %lld, %lld)", prefix_len, (long long)tree_seq_stride,
                   (long long)tree_row0);
@@ -357,7 +517,7 @@ int qattn_prefix_tree_fwd(const void* q, const int64_t q_stride[3], const void* 
     const int64_t ups = units_per_split(batch, num_kv_heads, max_seqlen, g);
     const int splits = prefix_splits(ups, prefix_len, num_splits, bps);
     const int64_t need = workspace_bytes(total_tokens, num_q_heads, head_dim, splits);
-    if (!workspace || workspace_size < need || ((uintptr_t)workspace & 255)) {
+    if (need > 0 && (!workspace || workspace_size < need || ((uintptr_t)workspace & 255))) {
         set_error("workspace of %lld bytes (256-byte aligned) required, got %lld", (long long)need,
                   (long long)workspace_size);
         return QATTN_ERR_WORKSPACE;
@@ -366,15 +526,18 @@ int qattn_prefix_tree_fwd(const void* q, const int64_t q_stride[3], const void* 
         set_error("too many prefix work units");
         return QATTN_ERR_ARG;
     }
+    const bool fused = splits == 1;
     const int64_t plane = total_tokens * num_q_heads;
     PrefixParams pp{};
     pp.q = q;
     pp.kp = k_prefix;
     pp.vp = v_prefix;
     pp.cu = cu_seqlens;
-    pp.part_m = (float*)workspace;
-    pp.part_l = (float*)((char*)workspace + align256(splits * plane * 4));
-    pp.part_acc = (float*)((char*)workspace + 2 * align256(splits * plane * 4));
+    if (!fused) {
+        pp.part_m = (float*)workspace;
+        pp.part_l = (float*)((char*)workspace + align256(splits * plane * 4));
+        pp.part_acc = (float*)((char*)workspace + 2 * align256(splits * plane * 4));
+    }
     pp.sq_t = q_stride[0];
     pp.sq_h = q_stride[1];
     pp.skp_b = kp_stride[0];
@@ -397,15 +560,15 @@ int qattn_prefix_tree_fwd(const void* q, const int64_t q_stride[3], const void* 
     pp.gdiv = make_divider(g);
     pp.scale_log2 = scale * kLog2e;
     if (dtype == QATTN_DTYPE_F16) {
-        rc = head_dim == 32 ? launch_prefix<F16, 32>(pp, st)
-             : head_dim == 64 ? launch_prefix<F16, 64>(pp, st)
-                              : launch_prefix<F16, 128>(pp, st);
+        rc = head_dim == 32   ? launch_prefix<F16, 32>(pp, tp, fused, st)
+             : head_dim == 64 ? launch_prefix<F16, 64>(pp, tp, fused, st)
+                              : launch_prefix<F16, 128>(pp, tp, fused, st);
     } else {
-        rc = head_dim == 32 ? launch_prefix<BF16, 32>(pp, st)
-             : head_dim == 64 ? launch_prefix<BF16, 64>(pp, st)
-                              : launch_prefix<BF16, 128>(pp, st);
+        rc = head_dim == 32   ? launch_prefix<BF16, 32>(pp, tp, fused, st)
+             : head_dim == 64 ? launch_prefix<BF16, 64>(pp, tp, fused, st)
+                              : launch_prefix<BF16, 128>(pp, tp, fused, st);
     }
-    if (rc) return rc;
+    if (rc || fused) return rc;
     tp.part_m = pp.part_m;
     tp.part_l = pp.part_l;
     tp.part_acc = pp.part_acc;

@@ -29,11 +29,11 @@
 
 #include "qattn_common.h"
 #include "qattn_device.h"
+#include "tree_walk.h"
 
 namespace qattn {
 
 constexpr int kThreads = 256;
-constexpr int kChunk = 8;          // ancestor steps whose loads are issued together
 #ifndef QATTN_SUBTREE_LDS_KB
 #define QATTN_SUBTREE_LDS_KB 48
 #endif
@@ -46,8 +46,6 @@ constexpr int kLdsBudget = QATTN_SUBTREE_LDS_KB * 1024;
 // Staging passes: kLdsBudget / (4 D) rows, 256 / (D / 8) rows per pass.
 constexpr int kMaxPass = kLdsBudget / 8192;
 
-enum { WALK_HEAP = 0, WALK_PARENTS = 1 };
-enum { KV_PACKED = 0, KV_PAGED = 1 };
 
 static thread_local char g_err[512];
 
@@ -61,110 +59,15 @@ void set_error(const char* fmt, ...) {
 void clear_error() { g_err[0] = 0; }
 
 // ---------------------------------------------------------------------------
-// Device helpers shared by the kernels
-// ---------------------------------------------------------------------------
-
-// Sequence bounds with the guards documented in qattn.h.
-__device__ __forceinline__ bool seq_bounds(const TreeParams& p, int seq, int32_t& start, int32_t& n) {
-    int32_t s = p.cu[seq], e = p.cu[seq + 1];
-    if (s < 0 || e < s || (int64_t)e > p.total_tokens) return false;
-    start = s;
-    n = e - s;
-    if (n > p.max_seqlen) n = p.max_seqlen;
-    return true;
-}
-
-__device__ __forceinline__ int64_t kv_base(const TreeParams& p, int seq, int32_t start) {
-    return p.kv_seq_stride ? (int64_t)seq * p.kv_seq_stride + p.kv_row0 : (int64_t)start;
-}
-
-// Next node of the walk (src/ragged_attn.py:376-377 heap, :692-694 parents).
-template <int WALK>
-__device__ __forceinline__ int32_t walk_next(const TreeParams& p, int32_t start, int32_t n, int32_t cur) {
-    if constexpr (WALK == WALK_HEAP) {
-        return heap_parent(cur, p.bdiv);
-    } else {
-        int32_t par = p.parents[start + cur];
-        return (par >= 0 && par < n) ? par : cur;
-    }
-}
-
-// Initial softmax state from split-K prefix partials (flash-decoding merge).
-template <int D>
-__device__ __forceinline__ void load_partial_state(const TreeParams& p, int64_t qrow, int h, int lane,
-                                                   float& m, float& l, float* acc) {
-    const int64_t plane = p.total_tokens * (int64_t)p.Hq;
-    const int64_t idx = qrow * p.Hq + h;
-    float m0 = -INFINITY;
-    for (int s = 0; s < p.n_split; ++s) m0 = fmaxf(m0, p.part_m[s * plane + idx]);
-    m = m0;
-    l = 0.f;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) acc[j] = 0.f;
-    if (m0 == -INFINITY) return;
-    for (int s = 0; s < p.n_split; ++s) {
-        const float w = fast_exp2(p.part_m[s * plane + idx] - m0);
-        l = __builtin_fmaf(w, p.part_l[s * plane + idx], l);
-        const float4* a = reinterpret_cast<const float4*>(p.part_acc + (s * plane + idx) * D + lane * 8);
-        float4 a0 = a[0], a1 = a[1];
-        acc[0] = __builtin_fmaf(w, a0.x, acc[0]);
-        acc[1] = __builtin_fmaf(w, a0.y, acc[1]);
-        acc[2] = __builtin_fmaf(w, a0.z, acc[2]);
-        acc[3] = __builtin_fmaf(w, a0.w, acc[3]);
-        acc[4] = __builtin_fmaf(w, a1.x, acc[4]);
-        acc[5] = __builtin_fmaf(w, a1.y, acc[5]);
-        acc[6] = __builtin_fmaf(w, a1.z, acc[6]);
-        acc[7] = __builtin_fmaf(w, a1.w, acc[7]);
-    }
-}
-
-// Fold one chunk of scores (log2 domain, -inf = not attended) into (m, l, acc).
-template <typename T, int CH>
-__device__ __forceinline__ void softmax_fold(float& m, float& l, float* acc, const float* sc, const Vec16* vr) {
-    float cmax = sc[0];
-#pragma unroll
-    for (int j = 1; j < CH; ++j) cmax = fmaxf(cmax, sc[j]);
-    const float m_new = fmaxf(m, cmax);
-    const float m_ref = (m_new == -INFINITY) ? 0.f : m_new;
-    const float alpha = fast_exp2(m - m_ref);
-    l *= alpha;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) acc[j] *= alpha;
-#pragma unroll
-    for (int j = 0; j < CH; ++j) {
-        const float pj = fast_exp2(sc[j] - m_ref);  // exp2(-inf) = 0 for skipped steps
-        l += pj;
-        axpy8<T>(acc, pj, vr[j]);
-    }
-    m = m_new;
-}
-
-// Normalise and write one output row group (+ LSE from lane 0).
-template <typename T, bool LSE>
-__device__ __forceinline__ void write_out(const TreeParams& p, int64_t qrow, int h, int lane,
-                                          float m, float l, float* acc) {
-    // l == 0 only for a query with no attended key; the reference divides by 1
-    // there (src/ragged_attn.py:379-380).
-    const float l_safe = (l == 0.f) ? 1.f : l;
-    const float inv = __builtin_amdgcn_rcpf(l_safe);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) acc[j] *= inv;
-    uint16_t* optr = (uint16_t*)p.o + qrow * p.so_t + (int64_t)h * p.so_h + lane * 8;
-    st16(optr, pack8<T>(acc));
-    if constexpr (LSE) {
-        if (lane == 0) p.lse[qrow * p.slse_t + (int64_t)h * p.slse_h] = (m + fast_log2(l_safe)) * kLn2;
-    }
-}
-
-// ---------------------------------------------------------------------------
-// Gather kernel
+// Gather kernel: 4 lanes per (token, q head), 64 pairs per workgroup with the
+// head index fastest, so a workgroup reads 2 tokens' contiguous head rows.
 // ---------------------------------------------------------------------------
 template <typename T, int D, int WALK, int LAYOUT, bool LSE, bool PSTATE>
 __global__ __launch_bounds__(kThreads) void tree_gather_kernel(TreeParams p) {
-    constexpr int LPR = D / 8;
-    constexpr int SLOTS = kThreads / LPR;
-    const int lane = threadIdx.x % LPR;
-    const int64_t slot = (int64_t)blockIdx.x * SLOTS + threadIdx.x / LPR;
+    constexpr int NCH = D / 32;
+    constexpr int SLOTS = kThreads / 4;
+    const int j = threadIdx.x & 3;
+    const int64_t slot = (int64_t)blockIdx.x * SLOTS + (threadIdx.x >> 2);
     const int h = (int)(slot % p.Hq);
     const int64_t rest = slot / p.Hq;
     const int tok = (int)(rest % p.max_seqlen);
@@ -173,113 +76,23 @@ __global__ __launch_bounds__(kThreads) void tree_gather_kernel(TreeParams p) {
     int32_t start, n;
     if (!seq_bounds(p, seq, start, n)) return;
     if (tok >= n) return;
-    const int kvh = h / p.group;
-    const int64_t kvb = kv_base(p, seq, start);
     const int64_t qrow = (int64_t)start + tok;
-
-    const uint16_t* kbase = (const uint16_t*)p.k + (int64_t)kvh * p.sk_h + lane * 8;
-    const uint16_t* vbase = (const uint16_t*)p.v + (int64_t)kvh * p.sv_h + lane * 8;
-    const Vec16 qv = ld16((const uint16_t*)p.q + qrow * p.sq_t + (int64_t)h * p.sq_h + lane * 8);
-
-    float m = -INFINITY, l = 0.f, acc[8];
+    Vec16 qf[NCH];
+    load_q4<D>(p, qrow, h, j, qf);
+    float m = -INFINITY, l = 0.f, acc[8 * NCH];
     if constexpr (PSTATE) {
-        load_partial_state<D>(p, qrow, h, lane, m, l, acc);
+        load_partial_state4<D>(p, qrow, h, j, m, l, acc);
     } else {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc[j] = 0.f;
+        for (int e = 0; e < 8 * NCH; ++e) acc[e] = 0.f;
     }
-
-    int32_t cur = tok, prev = -1;
-    for (int s0 = 0; s0 <= p.max_depth; s0 += kChunk) {
-        int64_t koff[kChunk], voff[kChunk];
-        bool val[kChunk];
-#pragma unroll
-        for (int j = 0; j < kChunk; ++j) {
-            bool ok = (s0 + j <= p.max_depth) && (cur != prev);
-            int64_t ko = 0, vo = 0;
-            if constexpr (LAYOUT == KV_PACKED) {
-                const int64_t row = kvb + cur;
-                ko = row * p.sk_t;
-                vo = row * p.sv_t;
-            } else {
-                const int32_t lp = cur / p.page_size;
-                const int32_t sl = cur - lp * p.page_size;
-                int32_t pg = -1;
-                if (ok && lp < p.pt_cols) pg = p.page_table[(int64_t)seq * p.pt_cols + lp];
-                ok = ok && pg >= 0 && pg < p.num_pages;
-                ko = (int64_t)pg * p.sk_page + (int64_t)sl * p.sk_t;
-                vo = (int64_t)pg * p.sv_page + (int64_t)sl * p.sv_t;
-            }
-            val[j] = ok;
-            koff[j] = ko;
-            voff[j] = vo;
-            prev = cur;
-            cur = walk_next<WALK>(p, start, n, cur);
-        }
-        Vec16 kr[kChunk], vr[kChunk];
-#pragma unroll
-        for (int j = 0; j < kChunk; ++j) {
-            kr[j] = Vec16{{0u, 0u, 0u, 0u}};
-            vr[j] = Vec16{{0u, 0u, 0u, 0u}};
-            if (val[j]) {
-                kr[j] = ld16(kbase + koff[j]);
-                vr[j] = ld16(vbase + voff[j]);
-            }
-        }
-        float sc[kChunk];
-#pragma unroll
-        for (int j = 0; j < kChunk; ++j) {
-            const float d = group_sum<LPR>(dot8<T>(qv, kr[j])) * p.scale_log2;
-            sc[j] = val[j] ? d : -INFINITY;
-        }
-        softmax_fold<T, kChunk>(m, l, acc, sc, vr);
-        // The walk is stalled (root reached / self-loop) for every lane.
-        if (!__any(cur != prev)) break;
-    }
-    write_out<T, LSE>(p, qrow, h, lane, m, l, acc);
+    gather_walk4<T, D, WALK, LAYOUT>(p, seq, start, n, tok, h / p.group, qf, j, m, l, acc);
+    write_out4<T, D, LSE>(p, qrow, h, j, m, l, acc);
 }
 
 // ---------------------------------------------------------------------------
 // Subtree kernel (heap walk, packed or hybrid K/V layout)
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ int rl(int v, int i) { return __builtin_amdgcn_readlane(v, i); }
-
-// Initial state from split-K partials for a 4-lane query group: lane j owns
-// the 16-byte chunks j, j+4, ... of the head row.
-template <int D>
-__device__ __forceinline__ void load_partial_state4(const TreeParams& p, int64_t qrow, int h, int j,
-                                                    float& m, float& l, float* acc) {
-    constexpr int NCH = D / 32;
-    const int64_t plane = p.total_tokens * (int64_t)p.Hq;
-    const int64_t idx = qrow * p.Hq + h;
-    float m0 = -INFINITY;
-    for (int s = 0; s < p.n_split; ++s) m0 = fmaxf(m0, p.part_m[s * plane + idx]);
-    m = m0;
-    l = 0.f;
-#pragma unroll
-    for (int e = 0; e < 8 * NCH; ++e) acc[e] = 0.f;
-    if (m0 == -INFINITY) return;
-    for (int s = 0; s < p.n_split; ++s) {
-        const float w = fast_exp2(p.part_m[s * plane + idx] - m0);
-        l = __builtin_fmaf(w, p.part_l[s * plane + idx], l);
-        const float* a = p.part_acc + (s * plane + idx) * D + 8 * j;
-#pragma unroll
-        for (int i = 0; i < NCH; ++i) {
-            const float4 a0 = *reinterpret_cast<const float4*>(a + 32 * i);
-            const float4 a1 = *reinterpret_cast<const float4*>(a + 32 * i + 4);
-            float* c = acc + 8 * i;
-            c[0] = __builtin_fmaf(w, a0.x, c[0]);
-            c[1] = __builtin_fmaf(w, a0.y, c[1]);
-            c[2] = __builtin_fmaf(w, a0.z, c[2]);
-            c[3] = __builtin_fmaf(w, a0.w, c[3]);
-            c[4] = __builtin_fmaf(w, a1.x, c[4]);
-            c[5] = __builtin_fmaf(w, a1.y, c[5]);
-            c[6] = __builtin_fmaf(w, a1.z, c[6]);
-            c[7] = __builtin_fmaf(w, a1.w, c[7]);
-        }
-    }
-}
-
 // Exactly NS consecutive ancestor steps of one query, straight-line so the
 // scheduler can issue every LDS read of the chunk ahead of its use: scores
 // first, then one max, then the exponentials and the V accumulation
@@ -348,25 +161,6 @@ __device__ __forceinline__ void subtree_query(const uint16_t* Ks, const uint16_t
             case 7: fold_chunk<T, D, 7>(Ks, Vs, qf, cur, lt, off, lam_min, bdiv, c, j, m, l, acc); break;
             default: fold_chunk<T, D, 8>(Ks, Vs, qf, cur, lt, off, lam_min, bdiv, c, j, m, l, acc); break;
         }
-    }
-}
-
-template <typename T, int D, bool LSE>
-__device__ __forceinline__ void write_out4(const TreeParams& p, int64_t qrow, int h, int j, float m, float l,
-                                           float* acc) {
-    constexpr int NCH = D / 32;
-    const float l_safe = (l == 0.f) ? 1.f : l;
-    const float inv = __builtin_amdgcn_rcpf(l_safe);
-    uint16_t* optr = (uint16_t*)p.o + qrow * p.so_t + (int64_t)h * p.so_h + 8 * j;
-#pragma unroll
-    for (int i = 0; i < NCH; ++i) {
-        float r[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) r[e] = acc[8 * i + e] * inv;
-        st16(optr + 32 * i, pack8<T>(r));
-    }
-    if constexpr (LSE) {
-        if (j == 0) p.lse[qrow * p.slse_t + (int64_t)h * p.slse_h] = (m + fast_log2(l_safe)) * kLn2;
     }
 }
 
@@ -759,7 +553,7 @@ static bool make_subtree_plan(int b, int64_t n, int max_depth, int rcap, Subtree
 
 template <typename T, int D, int WALK, int LAYOUT, bool LSE, bool PSTATE>
 static int launch_gather(const TreeParams& p, hipStream_t st) {
-    constexpr int SLOTS = kThreads / (D / 8);
+    constexpr int SLOTS = kThreads / 4;  // 4 lanes per (token, q head)
     const int64_t slots = (int64_t)p.B * p.max_seqlen * p.Hq;
     const int64_t blocks = (slots + SLOTS - 1) / SLOTS;
     if (blocks >= (int64_t(1) << 31)) {

@@ -1,0 +1,212 @@
+// tree_walk.h -- device-side pieces of the ancestor walk shared by the tree
+// kernels (tree_attn.hip) and the fused epilogue of the prefix kernel
+// (prefix_attn.hip).
+//
+// A query (token, q head) is owned by a group of 4 consecutive lanes; lane j
+// holds the 16-byte chunks j, j+4, j+8, ... of every D-element head row (Q, K,
+// V rows and the fp32 accumulator), so a chunk of the row is 64 contiguous
+// bytes per group and the dot-product reduction is a 2-step DPP quad sum.
+// Scores are kept in the log2 domain: s = (q . k) * scale * log2(e).
+#pragma once
+
+#include "qattn_common.h"
+#include "qattn_device.h"
+
+namespace qattn {
+
+enum { WALK_HEAP = 0, WALK_PARENTS = 1 };
+enum { KV_PACKED = 0, KV_PAGED = 1 };
+
+__device__ __forceinline__ int rl(int v, int i) { return __builtin_amdgcn_readlane(v, i); }
+
+// Sequence bounds with the guards documented in qattn.h.
+__device__ __forceinline__ bool seq_bounds(const TreeParams& p, int seq, int32_t& start, int32_t& n) {
+    int32_t s = p.cu[seq], e = p.cu[seq + 1];
+    if (s < 0 || e < s || (int64_t)e > p.total_tokens) return false;
+    start = s;
+    n = e - s;
+    if (n > p.max_seqlen) n = p.max_seqlen;
+    return true;
+}
+
+// First tree K/V row of a sequence: cu-packed, or the hybrid layout where each
+// sequence's tree rows follow its prefix rows.
+__device__ __forceinline__ int64_t kv_base(const TreeParams& p, int seq, int32_t start) {
+    return p.kv_seq_stride ? (int64_t)seq * p.kv_seq_stride + p.kv_row0 : (int64_t)start;
+}
+
+// Next node of the walk (src/ragged_attn.py:376-377 heap, :692-694 parents).
+template <int WALK>
+__device__ __forceinline__ int32_t walk_next(const TreeParams& p, int32_t start, int32_t n, int32_t cur) {
+    if constexpr (WALK == WALK_HEAP) {
+        return heap_parent(cur, p.bdiv);
+    } else {
+        const int32_t par = p.parents[start + cur];
+        return (par >= 0 && par < n) ? par : cur;
+    }
+}
+
+// Q fragment of a query in the 4-lane layout.
+template <int D>
+__device__ __forceinline__ void load_q4(const TreeParams& p, int64_t qrow, int h, int j, Vec16* qf) {
+    const uint16_t* qp = (const uint16_t*)p.q + qrow * p.sq_t + (int64_t)h * p.sq_h + 8 * j;
+#pragma unroll
+    for (int i = 0; i < D / 32; ++i) qf[i] = ld16(qp + 32 * i);
+}
+
+// Initial state from split-K prefix partials (flash-decoding merge of all
+// splits): m = max_s m_s, l = sum_s 2^(m_s - m) l_s, acc likewise.
+template <int D>
+__device__ __forceinline__ void load_partial_state4(const TreeParams& p, int64_t qrow, int h, int j,
+                                                    float& m, float& l, float* acc) {
+    constexpr int NCH = D / 32;
+    const int64_t plane = p.total_tokens * (int64_t)p.Hq;
+    const int64_t idx = qrow * p.Hq + h;
+    float m0 = -INFINITY;
+    for (int s = 0; s < p.n_split; ++s) m0 = fmaxf(m0, p.part_m[s * plane + idx]);
+    m = m0;
+    l = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8 * NCH; ++e) acc[e] = 0.f;
+    if (m0 == -INFINITY) return;
+    for (int s = 0; s < p.n_split; ++s) {
+        const float ms = p.part_m[s * plane + idx];
+        if (ms == -INFINITY) continue;
+        const float w = fast_exp2(ms - m0);
+        l = __builtin_fmaf(w, p.part_l[s * plane + idx], l);
+        const float* a = p.part_acc + (s * plane + idx) * D + 8 * j;
+#pragma unroll
+        for (int i = 0; i < NCH; ++i) {
+            const float4 a0 = *reinterpret_cast<const float4*>(a + 32 * i);
+            const float4 a1 = *reinterpret_cast<const float4*>(a + 32 * i + 4);
+            float* c = acc + 8 * i;
+            c[0] = __builtin_fmaf(w, a0.x, c[0]);
+            c[1] = __builtin_fmaf(w, a0.y, c[1]);
+            c[2] = __builtin_fmaf(w, a0.z, c[2]);
+            c[3] = __builtin_fmaf(w, a0.w, c[3]);
+            c[4] = __builtin_fmaf(w, a1.x, c[4]);
+            c[5] = __builtin_fmaf(w, a1.y, c[5]);
+            c[6] = __builtin_fmaf(w, a1.z, c[6]);
+            c[7] = __builtin_fmaf(w, a1.w, c[7]);
+        }
+    }
+}
+
+// Partial dot product of the lane's chunks, reduced over the 4-lane group.
+template <typename T, int NCH>
+__device__ __forceinline__ float qk4(const Vec16* qf, const Vec16* kf) {
+    float d = 0.f;
+#pragma unroll
+    for (int i = 0; i < NCH; ++i) d += dot8<T>(qf[i], kf[i]);
+    return group_sum<4>(d);
+}
+
+// Merge NS scores (log2 domain, -inf = not attended) and their V fragments
+// into (m, l, acc): one max, one rescale, NS exponentials.
+template <typename T, int NCH, int NS>
+__device__ __forceinline__ void fold_scores(const float* s, const Vec16 (*vf)[NCH], float& m, float& l,
+                                            float* acc) {
+    float cm = s[0];
+#pragma unroll
+    for (int t = 1; t < NS; ++t) cm = fmaxf(cm, s[t]);
+    const float m_new = fmaxf(m, cm);
+    if (m_new == -INFINITY) return;  // nothing attended yet
+    if (m != -INFINITY) {
+        const float alpha = fast_exp2(m - m_new);
+        l *= alpha;
+#pragma unroll
+        for (int e = 0; e < 8 * NCH; ++e) acc[e] *= alpha;
+    }
+#pragma unroll
+    for (int t = 0; t < NS; ++t) {
+        const float pt = fast_exp2(s[t] - m_new);  // exp2(-inf) = 0 for skipped steps
+        l += pt;
+#pragma unroll
+        for (int i = 0; i < NCH; ++i) axpy8<T>(acc + 8 * i, pt, vf[t][i]);
+    }
+    m = m_new;
+}
+
+// The ancestor walk of one query with K/V rows gathered from global memory:
+// steps s = 0..max_depth attend c_s iff c_s != c_{s-1} (src/ragged_attn.py:
+// 338-377 heap, :657-698 parents).  The loads of CH steps are issued together
+// before their scores are formed; the chunk loop stops once every lane's walk
+// has stalled (root reached or self-loop).
+template <typename T, int D, int WALK, int LAYOUT>
+__device__ __forceinline__ void gather_walk4(const TreeParams& p, int seq, int32_t start, int32_t n, int tok,
+                                             int kvh, const Vec16* qf, int j, float& m, float& l, float* acc) {
+    constexpr int NCH = D / 32;
+    constexpr int CH = 8 / NCH;  // 2 steps for D=128: 64 VGPRs of K/V loads in flight per lane
+    const int64_t kvb = kv_base(p, seq, start);
+    const uint16_t* kb = (const uint16_t*)p.k + (int64_t)kvh * p.sk_h + 8 * j;
+    const uint16_t* vb = (const uint16_t*)p.v + (int64_t)kvh * p.sv_h + 8 * j;
+    int32_t cur = tok, prev = -1;
+    for (int s0 = 0; s0 <= p.max_depth; s0 += CH) {
+        int64_t ko[CH], vo[CH];
+        bool val[CH];
+#pragma unroll
+        for (int t = 0; t < CH; ++t) {
+            bool ok = (s0 + t <= p.max_depth) && (cur != prev);
+            if constexpr (LAYOUT == KV_PACKED) {
+                ko[t] = (kvb + cur) * p.sk_t;
+                vo[t] = (kvb + cur) * p.sv_t;
+            } else {
+                const int32_t lp = cur / p.page_size;
+                const int32_t sl = cur - lp * p.page_size;
+                int32_t pg = -1;
+                if (ok && lp < p.pt_cols) pg = p.page_table[(int64_t)seq * p.pt_cols + lp];
+                ok = ok && pg >= 0 && pg < p.num_pages;
+                ko[t] = (int64_t)pg * p.sk_page + (int64_t)sl * p.sk_t;
+                vo[t] = (int64_t)pg * p.sv_page + (int64_t)sl * p.sv_t;
+            }
+            val[t] = ok;
+            prev = cur;
+            cur = walk_next<WALK>(p, start, n, cur);
+        }
+        Vec16 kf[CH][NCH], vf[CH][NCH];
+#pragma unroll
+        for (int t = 0; t < CH; ++t) {
+#pragma unroll
+            for (int i = 0; i < NCH; ++i) {
+                kf[t][i] = Vec16{{0u, 0u, 0u, 0u}};
+                vf[t][i] = Vec16{{0u, 0u, 0u, 0u}};
+                if (val[t]) {
+                    kf[t][i] = ld16(kb + ko[t] + 32 * i);
+                    vf[t][i] = ld16(vb + vo[t] + 32 * i);
+                }
+            }
+        }
+        float s[CH];
+#pragma unroll
+        for (int t = 0; t < CH; ++t) {
+            const float d = qk4<T, NCH>(qf, kf[t]) * p.scale_log2;
+            s[t] = val[t] ? d : -INFINITY;
+        }
+        fold_scores<T, NCH, CH>(s, vf, m, l, acc);
+        if (!__any(cur != prev)) break;
+    }
+}
+
+// Normalise and store one query's output (+ LSE from lane 0 of the group).
+template <typename T, int D, bool LSE>
+__device__ __forceinline__ void write_out4(const TreeParams& p, int64_t qrow, int h, int j, float m, float l,
+                                           float* acc) {
+    constexpr int NCH = D / 32;
+    // l == 0 only for a query with no attended key; the reference divides by 1
+    // there (src/ragged_attn.py:379-380).
+    const float l_safe = (l == 0.f) ? 1.f : l;
+    const float inv = __builtin_amdgcn_rcpf(l_safe);
+    uint16_t* optr = (uint16_t*)p.o + qrow * p.so_t + (int64_t)h * p.so_h + 8 * j;
+#pragma unroll
+    for (int i = 0; i < NCH; ++i) {
+        float r[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) r[e] = acc[8 * i + e] * inv;
+        st16(optr + 32 * i, pack8<T>(r));
+    }
+    if constexpr (LSE) {
+        if (j == 0) p.lse[qrow * p.slse_t + (int64_t)h * p.slse_h] = (m + fast_log2(l_safe)) * kLn2;
+    }
+}
+
+}  // namespace qattn

@@ -15,8 +15,8 @@ import pytest
 import torch
 
 from conftest import GOLDEN_DIR, make_inputs, num_tree_nodes, oracle_tree, tree_case
-from oracle import sdpa
-from oracle import clib
+from oracle import clib, sdpa
+from oracle import tree as otree
 
 pytestmark = pytest.mark.gpu
 
@@ -85,7 +85,7 @@ def test_hybrid_matches_reference_tests(B, b, d):
     o_ref, _, _ = oracle_tree(Q, K, V, cu, b, d, Kp=Kp, Vp=Vp)
     check_fp16(O.double().cpu().numpy(), o_ref, "hybrid L=32")
     # and the padded-SDPA restatement of the reference's own check (:444-469)
-    masks = [np.asarray(__import__("oracle.tree", fromlist=["x"]).tree_attention_mask(b, d))] * B
+    masks = [otree.tree_attention_mask(b, d)] * B
     O_sdpa = sdpa.packed_tree_attention(Q, K, V, cu, masks, Kp=Kp, Vp=Vp)
     assert torch.allclose(O.float().cpu(), O_sdpa, atol=1e-2, rtol=1e-2)
 
@@ -220,7 +220,6 @@ def test_cfg4_full_size():
     Q, K, V, cu = tree_case(B, b, d, Hq, D, Hkv=Hkv)
     Kp, Vp = _prefix(B, L, Hkv, D, B * 10000 + b * 100 + d + 1)
     O = ra.ragged_attention_prefix(Q.to(DEV), K.to(DEV), V.to(DEV), cu, Kp.to(DEV), Vp.to(DEV), b, d)
-    from oracle import tree as otree
     masks = [otree.tree_attention_mask(b, d)] * B
     ref = sdpa.packed_tree_attention(Q, K, V, cu, masks, Kp=Kp, Vp=Vp)
     check_fp16(O.double().cpu().numpy(), ref.double().numpy(), "cfg4")
@@ -238,7 +237,6 @@ def test_cfg5_sampled():
     O = ra.ragged_attention_prefix(Q.to(DEV), K.to(DEV), V.to(DEV), cu, Kp.to(DEV), Vp.to(DEV), b, d)
     O = O.cpu()
     assert torch.isfinite(O.float()).all()
-    from oracle import tree as otree
     m = otree.tree_attention_mask(b, d)
     for s in (0, 15):
         rows = slice(s * N, (s + 1) * N)

@@ -162,9 +162,11 @@ def test_gather_and_subtree_agree():
         Q, K, V, cu = tree_case(B, b, d, H, D)
         o1, l1 = run_tree(Q, K, V, cu, b, d, algo=1)
         o2, l2 = run_tree(Q, K, V, cu, b, d, algo=2)
-        # two fp16 roundings of values that differ by fp32 noise: <= 2 ulp
+        # two fp16 roundings of fp32 values that differ by summation-order
+        # noise (~1e-6 absolute): <= 2 ulp, with an absolute floor for
+        # results near zero where that noise exceeds an fp16 ulp
         ulp = 2.0 ** (np.floor(np.log2(np.maximum(np.abs(o1), 2.0 ** -14))) - 10)
-        bad = np.abs(o1 - o2) > 2 * ulp
+        bad = np.abs(o1 - o2) > 2 * ulp + 1e-5
         assert not bad.any(), f"{bad.sum()} elements differ by more than 2 ulp"
         assert np.abs(l1 - l2).max() <= 1e-5
 
