@@ -80,6 +80,35 @@ def model_costs(c):
     return tree_bytes + prefix_bytes, tree_flops + prefix_flops, prefix_flops
 
 
+def measured_traffic(config):
+    """HBM bytes per dispatch of the dominant kernel, from the committed counter
+    summary profiles/<kernel>_<config>_traffic.md (line 'hbm_bytes_per_dispatch: N'),
+    or None when no summary exists for this config."""
+    import glob
+    for path in sorted(glob.glob(os.path.join(ROOT, "profiles", f"*_{config}_traffic.md"))):
+        try:
+            for line in open(path):
+                if line.strip().startswith("hbm_bytes_per_dispatch:"):
+                    return int(float(line.split(":", 1)[1].strip().strip("`")))
+        except (OSError, ValueError):
+            pass
+    return None
+
+
+def copy_calibration(mib):
+    """A plain device copy of `mib` MiB (read mib, write mib): the reference
+    kernel for scaling FETCH_SIZE / WRITE_SIZE counters to bytes."""
+    import torch
+    n = mib << 20
+    x = torch.empty(n // 2, dtype=torch.float16, device="cuda").normal_()
+    y = torch.empty_like(x)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        y.copy_(x)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes": n, "copies": 3}), flush=True)
+
+
 def cpu_baseline(c, budget_s=20.0):
     """Reference CPU path on a bounded sample: padded SDPA (fp32, MATH) with
     the tree mask (prefix columns all-attend), repeated until ~budget_s."""
@@ -143,11 +172,16 @@ def main():
     ap.add_argument("--algo", default="auto", choices=["auto", "gather", "subtree"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--sets", type=int, default=0, help="rotating input sets (0: enough for > 512 MB)")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run a plain MIB-MiB device copy (counter calibration) and exit")
     args = ap.parse_args()
+    if args.copy_calibration:
+        copy_calibration(args.copy_calibration)
+        return
 
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
-              "the tree path shards over sequences/heads with no exchange (see DESIGN.md)", file=sys.stderr)
+              "the tree path shards over sequences/heads with no exchange between GPUs", file=sys.stderr)
         sys.exit(2)
 
     import torch
@@ -229,13 +263,7 @@ def main():
     else:
         roofline = {"bound": "hbm", "achieved": round(achieved_bw / 1e9, 1), "peak": PEAK_HBM / 1e9,
                     "unit": "GB/s", "frac": round(achieved_bw / PEAK_HBM, 4)}
-    traffic = None
-    prof = os.path.join(ROOT, "profiles", f"traffic_{args.config}.json")
-    if os.path.exists(prof):
-        try:
-            traffic = json.load(open(prof)).get("hbm_bytes_per_dispatch")
-        except (OSError, ValueError):
-            traffic = None
+    traffic = measured_traffic(args.config)
     roofline.update({"traffic": traffic, "algorithmic_bytes": alg_bytes, "flops": flops})
 
     cpu = None

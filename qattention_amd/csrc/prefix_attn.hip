@@ -95,7 +95,7 @@ __device__ __forceinline__ int vt_col(int k) {
 }
 
 template <typename T, int D, bool FUSED, bool LSE>
-__global__ __launch_bounds__(kPrefixThreads) __attribute__((amdgpu_waves_per_eu(1, 2))) void prefix_attn_kernel(
+__global__ __launch_bounds__(kPrefixThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefix_attn_kernel(
     PrefixParams p, TreeParams tp) {
     constexpr int NC = D / 32;      // MFMA k-chunks over the head dim
     constexpr int ND = D / 16;      // output tiles over the head dim
@@ -175,14 +175,16 @@ __global__ __launch_bounds__(kPrefixThreads) __attribute__((amdgpu_waves_per_eu(
     constexpr int KU = kBN * DV / kPrefixThreads;                        // K vectors per thread
     constexpr int VUNITS = (kBN / 4) * DV;                                // 4-key x 8-dim V units
     constexpr int VU = (VUNITS + kPrefixThreads - 1) / kPrefixThreads;   // V units per thread
+    static_assert((kBN * DV) % kPrefixThreads == 0 && (VUNITS % 64) == 0, "staging must tile whole waves");
     Vec16 kreg[KU], vreg[VU][4];
+    // Keys of the tail block beyond k_hi load row k_hi - 1 instead (always
+    // inside the split); their scores are masked to -inf, so P = 0 there.
     auto load_block = [&](int kb) {
 #pragma unroll
         for (int i = 0; i < KU; ++i) {
             const int u = tid + i * kPrefixThreads;
-            const int key = u / DV, ch = u % DV;
-            kreg[i] = Vec16{{0u, 0u, 0u, 0u}};
-            if (kb + key < k_hi) kreg[i] = ld16(kbase + (int64_t)(kb + key) * p.skp_t + 8 * ch);
+            const int key = min(kb + u / DV, k_hi - 1), ch = u % DV;
+            kreg[i] = ld16(kbase + (int64_t)key * p.skp_t + 8 * ch);
         }
 #pragma unroll
         for (int i = 0; i < VU; ++i) {
@@ -190,9 +192,8 @@ __global__ __launch_bounds__(kPrefixThreads) __attribute__((amdgpu_waves_per_eu(
             const int kg = u % (kBN / 4), dch = u / (kBN / 4);
 #pragma unroll
             for (int rk = 0; rk < 4; ++rk) {
-                const int key = kb + 4 * kg + rk;
-                vreg[i][rk] = Vec16{{0u, 0u, 0u, 0u}};
-                if (u < VUNITS && key < k_hi) vreg[i][rk] = ld16(vbase + (int64_t)key * p.svp_t + 8 * dch);
+                const int key = min(kb + 4 * kg + rk, k_hi - 1);
+                if (u < VUNITS) vreg[i][rk] = ld16(vbase + (int64_t)key * p.svp_t + 8 * dch);  // wave-uniform
             }
         }
     };
@@ -318,14 +319,20 @@ __global__ __launch_bounds__(kPrefixThreads) __attribute__((amdgpu_waves_per_eu(
         }
     };
 
-    for (int kb = k_lo; kb < k_hi; kb += kBN) {
+    // Full blocks in the loop, the split's partial tail block peeled after it,
+    // so the loop body is one straight-line copy of compute_block.
+    int kb = k_lo;
+    for (; kb + kBN <= k_hi; kb += kBN) {
         store_block();
         __syncthreads();
         if (kb + kBN < k_hi) load_block(kb + kBN);
-        if (kb + kBN <= k_hi)
-            compute_block(kb, std::false_type{});
-        else
-            compute_block(kb, std::true_type{});
+        compute_block(kb, std::false_type{});
+        __syncthreads();
+    }
+    if (kb < k_hi) {
+        store_block();
+        __syncthreads();
+        compute_block(kb, std::true_type{});
         __syncthreads();
     }
 

@@ -463,8 +463,11 @@ int launch_status(const char* what) {
     return QATTN_OK;
 }
 
-// Subtree tiling plan for a heap tree of n nodes (see DESIGN.md for the
-// derivation).  Returns false when no plan fits the LDS budget.
+// Subtree tiling plan for a heap tree of n nodes.  Level l of the heap holds
+// b^l nodes; a band of levels [lo, hi) is cut into tiles of G roots at level
+// lo whose subtrees (down to hi) plus one ancestor row per level above lo fit
+// the LDS budget.  Bands are chosen bottom-up, each the tallest that fits a
+// single-root subtree.  Returns false when no plan fits the LDS budget.
 static bool make_subtree_plan(int b, int64_t n, int max_depth, int rcap, SubtreePlan& plan) {
     plan = SubtreePlan{};
     if (n <= 0 || b < 1) return false;
