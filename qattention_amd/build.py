@@ -17,7 +17,7 @@ import sys
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(PKG_DIR, "csrc")
 LIB_PATH = os.path.join(PKG_DIR, "libqattn.so")
-SOURCES = ["tree_attn.hip", "prefix_attn.hip"]
+SOURCES = ["tree_attn.hip", "subtree_stream.hip", "prefix_attn.hip"]
 HEADERS = ["qattn_common.h", "qattn_device.h", "tree_walk.h"]
 ARCH = os.environ.get("QATTN_ARCH", "gfx950")
 

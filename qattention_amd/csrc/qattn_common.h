@@ -85,13 +85,32 @@ constexpr int kMaxBands = 32;
 struct Band {
     int32_t lo, hi, G, tile_base;
 };
+// Kernel argument form of the plan: the band of a tile is found with one
+// branch-free pass over tile_base[] (independent scalar loads) and one more
+// load of its packed (lo, hi, G).
 struct SubtreePlan {
     int32_t nbands;
     int32_t total_tiles;
-    int32_t max_rows;     // LDS rows (K and V each) of the largest tile
-    int32_t chain_h;      // b == 1: levels per tile
-    Band band[kMaxBands];
+    int32_t max_rows;                 // LDS rows (K and V each) of the largest tile
+    int32_t chain_h;                  // b == 1: levels per tile
+    int32_t tile_base[kMaxBands];     // first tile of band i; INT32_MAX past the last band
+    uint32_t band[kMaxBands];         // lo | hi << 8 | G << 16
 };
+
+// Launch arguments of the persistent subtree kernel (subtree_stream.hip).
+struct StreamArgs {
+    int32_t n_work;     // tiles over all (sequence, kv head) pairs
+    Divider tiles_div;  // tiles per (sequence, kv head)
+    Divider hkv_div;    // kv heads
+    Divider gdiv;       // q heads per kv head
+};
+
+// Subtree kernel: rows one tile may stage (K/V rows, Q rows) for head_dim,
+// and the largest batch it takes (its LDS copy of cu_seqlens).
+void stream_tile_caps(int head_dim, int* kv_rows, int* q_rows);
+int stream_max_batch();
+int launch_stream(const TreeParams& p, const SubtreePlan& plan, int dtype, int head_dim, bool pstate,
+                  hipStream_t st);
 
 void set_error(const char* fmt, ...);
 void clear_error();

@@ -10,13 +10,14 @@
 //                         heap walk, the explicit-parent walk and the paged
 //                         K/V layout, and merges split-K prefix partial states.
 //
-//  * tree_subtree_kernel  heap trees only.  A workgroup owns one subtree tile
-//                         (a band of BFS levels under G adjacent roots) of one
-//                         (sequence, kv head).  It stages the tile's K/V rows and
-//                         the few ancestor rows above it in LDS once, so every
-//                         ancestor read of every query in the tile is an LDS
-//                         read and each K/V row leaves HBM once per kv head.
-//                         All q heads of a GQA group share the staged rows.
+//  * tree_stream_kernel   heap trees only (subtree_stream.hip).  Persistent
+//                         workgroups walk subtree tiles (a band of BFS levels
+//                         under G adjacent roots) of each (sequence, kv head),
+//                         staging the tile's K/V rows, the few ancestor rows
+//                         above it and its Q rows in LDS while the previous
+//                         tile is computed, so each K/V row leaves HBM once per
+//                         kv head.  All q heads of a GQA group share the rows.
+//                         This file holds its tiling plan (make_subtree_plan).
 //
 // Scores are kept in the log2 domain (scale * log2(e) folded into one multiply)
 // and exponentiated with v_exp_f32.  Dot products use v_dot2_f32_{f16,bf16};
@@ -34,18 +35,6 @@
 namespace qattn {
 
 constexpr int kThreads = 256;
-#ifndef QATTN_SUBTREE_LDS_KB
-#define QATTN_SUBTREE_LDS_KB 48
-#endif
-#ifndef QATTN_SUBTREE_WAVES_PER_EU
-#define QATTN_SUBTREE_WAVES_PER_EU 3
-#endif
-// Bytes of K+V rows staged per subtree tile (a tuning constant: the tile size
-// trades workgroups per CU against ancestor rows re-read above each tile).
-constexpr int kLdsBudget = QATTN_SUBTREE_LDS_KB * 1024;
-// Staging passes: kLdsBudget / (4 D) rows, 256 / (D / 8) rows per pass.
-constexpr int kMaxPass = kLdsBudget / 8192;
-
 
 static thread_local char g_err[512];
 
@@ -88,279 +77,6 @@ __global__ __launch_bounds__(kThreads) void tree_gather_kernel(TreeParams p) {
     }
     gather_walk4<T, D, WALK, LAYOUT>(p, seq, start, n, tok, h / p.group, qf, j, m, l, acc);
     write_out4<T, D, LSE>(p, qrow, h, j, m, l, acc);
-}
-
-// ---------------------------------------------------------------------------
-// Subtree kernel (heap walk, packed or hybrid K/V layout)
-// ---------------------------------------------------------------------------
-// Exactly NS consecutive ancestor steps of one query, straight-line so the
-// scheduler can issue every LDS read of the chunk ahead of its use: scores
-// first, then one max, then the exponentials and the V accumulation
-// (two-phase softmax), merged into (m, l, acc) online.
-template <typename T, int D, int NS>
-__device__ __forceinline__ void fold_chunk(const uint16_t* Ks, const uint16_t* Vs, const Vec16* qf, int32_t& cur,
-                                           int lam_t0, int off, int lam_min, const Divider& bdiv, float c, int j,
-                                           float& m, float& l, float* acc) {
-    constexpr int NCH = D / 32;
-    int rows[NS];
-    float s[NS];
-#pragma unroll
-    for (int t = 0; t < NS; ++t) {
-        rows[t] = cur + rl(off, lam_t0 - t - lam_min);
-        cur = heap_parent(cur, bdiv);
-    }
-#pragma unroll
-    for (int t = 0; t < NS; ++t) {
-        const uint16_t* kr = Ks + (size_t)rows[t] * D + 8 * j;
-        float d = 0.f;
-#pragma unroll
-        for (int i = 0; i < NCH; ++i) d += dot8<T>(qf[i], ld16(kr + 32 * i));
-        s[t] = group_sum<4>(d) * c;
-    }
-    float cm = s[0];
-#pragma unroll
-    for (int t = 1; t < NS; ++t) cm = fmaxf(cm, s[t]);
-    const float m_new = fmaxf(m, cm);
-    if (m != -INFINITY) {
-        const float alpha = fast_exp2(m - m_new);
-        l *= alpha;
-#pragma unroll
-        for (int e = 0; e < 8 * NCH; ++e) acc[e] *= alpha;
-    }
-#pragma unroll
-    for (int t = 0; t < NS; ++t) {
-        const float pt = fast_exp2(s[t] - m_new);
-        l += pt;
-        const uint16_t* vr = Vs + (size_t)rows[t] * D + 8 * j;
-#pragma unroll
-        for (int i = 0; i < NCH; ++i) axpy8<T>(acc + 8 * i, pt, ld16(vr + 32 * i));
-    }
-    m = m_new;
-}
-
-// One query of a subtree tile: walk nsteps ancestors (all staged in LDS) in
-// chunks of at most 8 steps.  Level offsets: the LDS row of node x at level mu
-// is x + off[mu - lam_min] (one level per lane; mu is wave-uniform, so the
-// lookup is a readlane).  nsteps is wave-uniform, so the switch is a scalar
-// branch.
-template <typename T, int D>
-__device__ __forceinline__ void subtree_query(const uint16_t* Ks, const uint16_t* Vs, const Vec16* qf, int node,
-                                              int lam, int nsteps, int off, int lam_min, const Divider& bdiv,
-                                              float c, int j, float& m, float& l, float* acc) {
-    int32_t cur = node;
-    for (int t0 = 0; t0 < nsteps; t0 += 8) {
-        const int cnt = (nsteps - t0 < 8) ? nsteps - t0 : 8;
-        const int lt = lam - t0;
-        switch (cnt) {
-            case 1: fold_chunk<T, D, 1>(Ks, Vs, qf, cur, lt, off, lam_min, bdiv, c, j, m, l, acc); break;
-            case 2: fold_chunk<T, D, 2>(Ks, Vs, qf, cur, lt, off, lam_min, bdiv, c, j, m, l, acc); break;
-            case 3: fold_chunk<T, D, 3>(Ks, Vs, qf, cur, lt, off, lam_min, bdiv, c, j, m, l, acc); break;
-            case 4: fold_chunk<T, D, 4>(Ks, Vs, qf, cur, lt, off, lam_min, bdiv, c, j, m, l, acc); break;
-            case 5: fold_chunk<T, D, 5>(Ks, Vs, qf, cur, lt, off, lam_min, bdiv, c, j, m, l, acc); break;
-            case 6: fold_chunk<T, D, 6>(Ks, Vs, qf, cur, lt, off, lam_min, bdiv, c, j, m, l, acc); break;
-            case 7: fold_chunk<T, D, 7>(Ks, Vs, qf, cur, lt, off, lam_min, bdiv, c, j, m, l, acc); break;
-            default: fold_chunk<T, D, 8>(Ks, Vs, qf, cur, lt, off, lam_min, bdiv, c, j, m, l, acc); break;
-        }
-    }
-}
-
-// At most 3 workgroups of 48 KB LDS fit a CU, so the register budget may be
-// sized for 3 waves per SIMD (up to 168 VGPRs) to keep more LDS reads in flight.
-template <typename T, int D, bool LSE, bool PSTATE>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, QATTN_SUBTREE_WAVES_PER_EU))) void tree_subtree_kernel(TreeParams p, SubtreePlan plan, Divider gdiv) {
-    constexpr int LPR = D / 8;             // staging: lanes per 16-byte-vector row
-    constexpr int SLOTS = kThreads / LPR;  // staging: rows per pass
-    constexpr int NCH = D / 32;            // compute: 16-byte chunks per lane (4 lanes per query)
-    extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
-    uint16_t* Ks = smem;
-    uint16_t* Vs = smem + (size_t)plan.max_rows * D;
-
-    const int lane = threadIdx.x % LPR;
-    const int rg = threadIdx.x / LPR;
-    const int lane64 = threadIdx.x & 63;
-
-    const int kvh = blockIdx.x % p.Hkv;
-    const int rest = blockIdx.x / p.Hkv;
-    const int tile = rest % plan.total_tiles;
-    const int seq = rest / plan.total_tiles;
-    if (seq >= p.B) return;
-    int32_t start, n;
-    if (!seq_bounds(p, seq, start, n)) return;
-    if (n <= 0) return;
-    const int b = p.bdiv.d;
-
-    // ---- which band / roots ------------------------------------------------
-    int lo = 0, hi = 0, G = 1, tbase = 0;
-#pragma unroll
-    for (int i = 0; i < kMaxBands; ++i) {
-        if (i < plan.nbands && tile >= plan.band[i].tile_base) {
-            lo = plan.band[i].lo;
-            hi = plan.band[i].hi;
-            G = plan.band[i].G;
-            tbase = plan.band[i].tile_base;
-        }
-    }
-    int64_t r0, r1;  // root range [r0, r1) at level lo
-    if (b == 1) {
-        lo = (tile - tbase) * plan.chain_h;
-        hi = lo + plan.chain_h - 1;
-        r0 = lo;
-        r1 = lo + 1;
-    } else {
-        int64_t s_lo = 0, w_lo = 1;
-        for (int i = 0; i < lo; ++i) {
-            s_lo += w_lo;
-            w_lo *= b;
-        }
-        const int64_t i0 = (int64_t)(tile - tbase) * G;
-        r0 = s_lo + i0;
-        r1 = s_lo + ((i0 + G < w_lo) ? i0 + G : w_lo);
-    }
-    if (r0 >= n) return;
-    if (r1 > n) r1 = n;
-
-    // ---- level table, one level per lane (lane 0 = level lam_min) ----------
-    const int lam_min = (lo - p.max_depth > 0) ? lo - p.max_depth : 0;
-    const int nlev = hi - lam_min + 1;  // <= 64, guaranteed by the host plan
-    int first = 0, cnt = 0;
-    if (lane64 < nlev) {
-        const int lam = lam_min + lane64;
-        int64_t f, la;
-        if (lam >= lo) {
-            const int jj = lam - lo;
-            int64_t bj = 1, sj = 0;
-            for (int i = 0; i < jj; ++i) {
-                sj += bj;
-                bj *= b;
-            }
-            f = r0 * bj + sj;
-            la = r1 * bj + sj - 1;
-        } else {
-            int32_t a = (int32_t)r0, c = (int32_t)(r1 - 1);
-            for (int i = 0; i < lo - lam; ++i) {
-                a = heap_parent(a, p.bdiv);
-                c = heap_parent(c, p.bdiv);
-            }
-            f = a;
-            la = c;
-        }
-        if (la > n - 1) la = n - 1;
-        if (f <= la) {
-            first = (int)f;
-            cnt = (int)(la - f + 1);
-        }
-    }
-    int base = 0;
-    for (int i = 0; i < nlev; ++i) {
-        const int c = rl(cnt, i);
-        base += (i < lane64) ? c : 0;
-    }
-    const int off = base - first;  // LDS row of node x at this level = x + off
-    const int total_rows = rl(base + cnt, nlev - 1);
-    if (total_rows > plan.max_rows) return;  // cannot happen for a host-built plan
-
-    const int64_t kvb = kv_base(p, seq, start);
-    const uint16_t* kg = (const uint16_t*)p.k + (int64_t)kvh * p.sk_h + lane * 8;
-    const uint16_t* vg = (const uint16_t*)p.v + (int64_t)kvh * p.sv_h + lane * 8;
-
-    // ---- stage K/V rows: all global loads issued before the first LDS write --
-    Vec16 kst[kMaxPass], vst[kMaxPass];
-    int offr[kMaxPass];
-#pragma unroll
-    for (int ps = 0; ps < kMaxPass; ++ps) offr[ps] = rl(off, 0);
-    for (int i = 1; i < nlev; ++i) {
-        const int bi = rl(base, i), oi = rl(off, i), ci = rl(cnt, i);
-#pragma unroll
-        for (int ps = 0; ps < kMaxPass; ++ps) {
-            const int r = ps * SLOTS + rg;
-            if (ci > 0 && r >= bi) offr[ps] = oi;
-        }
-    }
-#pragma unroll
-    for (int ps = 0; ps < kMaxPass; ++ps) {
-        const int r = ps * SLOTS + rg;
-        if (r < total_rows) {
-            const int64_t row = kvb + (r - offr[ps]);
-            kst[ps] = ld16(kg + row * p.sk_t);
-            vst[ps] = ld16(vg + row * p.sv_t);
-        }
-    }
-
-    // ---- query schedule: 16 (node, q head) pairs per wave item; a wave item
-    // never spans two levels, so its step count is wave-uniform -----------------
-    const int g = p.group;
-    // readfirstlane tells the compiler the wave index is wave-uniform, which
-    // keeps the whole query schedule (levels, step counts) in scalar registers
-    // and the ancestor loop free of divergent branches.
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int grp = lane64 >> 2;
-    const int j = lane64 & 3;
-    const int lam_l = lam_min + lane64;
-    const int nw = (lane64 < nlev && lam_l >= lo) ? (cnt * g + 15) / 16 : 0;  // wave items per level
-    auto advance = [&](int& L, int& k) {
-        while (L <= hi) {
-            const int w = rl(nw, L - lam_min);
-            if (k < w) break;
-            k -= w;
-            ++L;
-        }
-    };
-    auto load_q = [&](int L, int k, Vec16* dst) {
-        const int s = k * 16 + grp;
-        if (s < rl(cnt, L - lam_min) * g) {
-            const int node = rl(first, L - lam_min) + divide(s, gdiv);
-            const int qh = kvh * g + (s - divide(s, gdiv) * g);
-            const uint16_t* qp = (const uint16_t*)p.q + ((int64_t)start + node) * p.sq_t + (int64_t)qh * p.sq_h + 8 * j;
-#pragma unroll
-            for (int i = 0; i < NCH; ++i) dst[i] = ld16(qp + 32 * i);
-        }
-    };
-    int L = lo, k = wave;
-    advance(L, k);
-    Vec16 qcur[NCH], qnext[NCH];
-#pragma unroll
-    for (int i = 0; i < NCH; ++i) qcur[i] = qnext[i] = Vec16{{0u, 0u, 0u, 0u}};
-    if (L <= hi) load_q(L, k, qcur);
-
-#pragma unroll
-    for (int ps = 0; ps < kMaxPass; ++ps) {
-        const int r = ps * SLOTS + rg;
-        if (r < total_rows) {
-            st16(Ks + (size_t)r * D + lane * 8, kst[ps]);
-            st16(Vs + (size_t)r * D + lane * 8, vst[ps]);
-        }
-    }
-    __syncthreads();
-
-    while (L <= hi) {
-        int Ln = L, kn = k + kThreads / 64;
-        advance(Ln, kn);
-        if (Ln <= hi) load_q(Ln, kn, qnext);
-
-        const int s = k * 16 + grp;
-        if (s < rl(cnt, L - lam_min) * g) {
-            const int node = rl(first, L - lam_min) + divide(s, gdiv);
-            const int qh = kvh * g + (s - divide(s, gdiv) * g);
-            const int64_t qrow = (int64_t)start + node;
-            float m = -INFINITY, l = 0.f, acc[8 * NCH];
-            if constexpr (PSTATE) {
-                load_partial_state4<D>(p, qrow, qh, j, m, l, acc);
-            } else {
-#pragma unroll
-                for (int e = 0; e < 8 * NCH; ++e) acc[e] = 0.f;
-            }
-            // steps t = 0..min(L, max_depth) attend levels L - t; the heap walk
-            // strictly decreases until the root, so these are exactly the steps
-            // with c_t != c_{t-1} (src/ragged_attn.py:338-377).
-            const int nsteps = (L < p.max_depth ? L : p.max_depth) + 1;
-            subtree_query<T, D>(Ks, Vs, qcur, node, L, nsteps, off, lam_min, p.bdiv, p.scale_log2, j, m, l, acc);
-            write_out4<T, D, LSE>(p, qrow, qh, j, m, l, acc);
-        }
-#pragma unroll
-        for (int i = 0; i < NCH; ++i) qcur[i] = qnext[i];
-        L = Ln;
-        k = kn;
-    }
 }
 
 // ---------------------------------------------------------------------------
@@ -468,18 +184,20 @@ int launch_status(const char* what) {
 // lo whose subtrees (down to hi) plus one ancestor row per level above lo fit
 // the LDS budget.  Bands are chosen bottom-up, each the tallest that fits a
 // single-root subtree.  Returns false when no plan fits the LDS budget.
-static bool make_subtree_plan(int b, int64_t n, int max_depth, int rcap, SubtreePlan& plan) {
+static bool make_subtree_plan(int b, int64_t n, int max_depth, int rcap, int ncap, SubtreePlan& plan) {
     plan = SubtreePlan{};
+    for (int i = 0; i < kMaxBands; ++i) plan.tile_base[i] = INT32_MAX;
     if (n <= 0 || b < 1) return false;
     if (b == 1) {
         const int extra = (int)std::min<int64_t>(max_depth, n - 1);
-        int h = rcap - extra;
+        int h = std::min(rcap - extra, ncap);
         h = std::min(h, 64 - extra);
         if (h < 1) return false;
         h = (int)std::min<int64_t>(h, n);
         plan.nbands = 1;
         plan.chain_h = h;
-        plan.band[0] = Band{0, (int32_t)(n - 1), 1, 0};
+        plan.tile_base[0] = 0;
+        plan.band[0] = 1u << 16;  // lo, hi come from chain_h for b == 1
         const int64_t tiles = (n + h - 1) / h;
         if (tiles >= (int64_t(1) << 30)) return false;
         plan.total_tiles = (int32_t)tiles;
@@ -523,7 +241,7 @@ static bool make_subtree_plan(int b, int64_t n, int max_depth, int rcap, Subtree
         for (int h = 1; h <= hi + 1; ++h) {
             const int lo = hi - h + 1;
             const int nlev = hi - std::max(0, lo - max_depth) + 1;
-            if (subtree(h) + extra_rows(1, lo) > rcap || nlev > 64) break;
+            if (subtree(h) + extra_rows(1, lo) > rcap || subtree(h) > ncap || nlev > 64) break;
             best = h;
         }
         if (best == 0) return false;
@@ -531,7 +249,7 @@ static bool make_subtree_plan(int b, int64_t n, int max_depth, int rcap, Subtree
         const int64_t size = subtree(best);
         const int64_t wlo = width(lo);
         int64_t G = 1;
-        while (G < wlo && (G + 1) * size + extra_rows(G + 1, lo) <= rcap) ++G;
+        while (G < wlo && (G + 1) * size + extra_rows(G + 1, lo) <= rcap && (G + 1) * size <= ncap) ++G;
         bands.push_back(Band{lo, hi, (int32_t)G, 0});
         if ((int)bands.size() > kMaxBands) return false;
         hi = lo - 1;
@@ -544,7 +262,9 @@ static bool make_subtree_plan(int b, int64_t n, int max_depth, int rcap, Subtree
         const int64_t wlo = width(bd.lo);
         tiles += (wlo + bd.G - 1) / bd.G;
         rows = std::max<int64_t>(rows, bd.G * subtree(bd.hi - bd.lo + 1) + extra_rows(bd.G, bd.lo));
-        plan.band[i] = bd;
+        if (bd.hi > 255 || bd.G > 65535) return false;
+        plan.tile_base[i] = bd.tile_base;
+        plan.band[i] = (uint32_t)bd.lo | ((uint32_t)bd.hi << 8) | ((uint32_t)bd.G << 16);
     }
     if (tiles >= (int64_t(1) << 30)) return false;
     plan.nbands = (int32_t)bands.size();
@@ -568,44 +288,26 @@ static int launch_gather(const TreeParams& p, hipStream_t st) {
     return launch_status("tree_gather_kernel");
 }
 
-template <typename T, int D, bool LSE, bool PSTATE>
-static int launch_subtree(const TreeParams& p, const SubtreePlan& plan, hipStream_t st) {
-    const int64_t blocks = (int64_t)p.B * p.Hkv * plan.total_tiles;
-    if (blocks >= (int64_t(1) << 31)) {
-        set_error("grid too large (%lld blocks)", (long long)blocks);
-        return QATTN_ERR_ARG;
-    }
-    const size_t lds = (size_t)plan.max_rows * D * 2 * sizeof(uint16_t);
-    hipLaunchKernelGGL((tree_subtree_kernel<T, D, LSE, PSTATE>), dim3((unsigned)blocks), dim3(kThreads), lds, st, p,
-                       plan, make_divider(p.group));
-    return launch_status("tree_subtree_kernel");
-}
-
 template <typename T, int D>
 static int dispatch_tree(const TreeParams& p, int walk, int layout, bool lse, bool pstate, int algo,
                          hipStream_t st) {
     if (walk == WALK_HEAP && layout == KV_PACKED && algo != QATTN_ALGO_GATHER) {
         SubtreePlan plan;
-        const int rcap = kLdsBudget / (4 * D);
-        const bool ok = make_subtree_plan(p.bdiv.d, p.max_seqlen, p.max_depth, rcap, plan);
+        int rcap = 0, qcap = 0;
+        stream_tile_caps(D, &rcap, &qcap);
+        const bool ok = p.B <= stream_max_batch() &&
+                        make_subtree_plan(p.bdiv.d, p.max_seqlen, p.max_depth, rcap, qcap / p.group, plan);
         const int64_t wgs = ok ? (int64_t)p.B * p.Hkv * plan.total_tiles : 0;
         // The subtree kernel needs enough tiles to fill 256 CUs; a merged
         // prefix state makes each query heavier, so it only pays off there
         // when tiles are plentiful.
         const bool use = ok && (algo == QATTN_ALGO_SUBTREE || wgs >= (pstate ? 2048 : 512));
         if (algo == QATTN_ALGO_SUBTREE && !ok) {
-            set_error("no subtree plan fits (b=%d, max_seqlen=%d, max_depth=%d)", p.bdiv.d, p.max_seqlen,
-                      p.max_depth);
+            set_error("no subtree plan fits (b=%d, max_seqlen=%d, max_depth=%d, batch=%d)", p.bdiv.d,
+                      p.max_seqlen, p.max_depth, p.B);
             return QATTN_ERR_ARG;
         }
-        if (use) {
-            if (lse) {
-                return pstate ? launch_subtree<T, D, true, true>(p, plan, st)
-                              : launch_subtree<T, D, true, false>(p, plan, st);
-            }
-            return pstate ? launch_subtree<T, D, false, true>(p, plan, st)
-                          : launch_subtree<T, D, false, false>(p, plan, st);
-        }
+        if (use) return launch_stream(p, plan, T::kCode, D, pstate, st);
     } else if (algo == QATTN_ALGO_SUBTREE) {
         set_error("the subtree kernel supports the heap walk on packed K/V only");
         return QATTN_ERR_ARG;
