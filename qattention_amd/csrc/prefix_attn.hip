@@ -52,48 +52,6 @@ struct PrefixParams {
     float scale_log2;
 };
 
-template <typename T>
-struct MfmaOps;
-
-template <>
-struct MfmaOps<F16> {
-    static __device__ __forceinline__ f4_t mma(const Vec16& a, const Vec16& b, f4_t c) {
-        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8_t, a), __builtin_bit_cast(h8_t, b), c, 0,
-                                                     0, 0);
-    }
-    static __device__ __forceinline__ uint32_t pack2(float x, float y) {
-        h2_t h;
-        h[0] = (_Float16)x;
-        h[1] = (_Float16)y;
-        return __builtin_bit_cast(uint32_t, h);
-    }
-};
-
-template <>
-struct MfmaOps<BF16> {
-    static __device__ __forceinline__ f4_t mma(const Vec16& a, const Vec16& b, f4_t c) {
-        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(b8_t, a), __builtin_bit_cast(b8_t, b), c, 0,
-                                                      0, 0);
-    }
-    static __device__ __forceinline__ uint32_t pack2(float x, float y) {
-        b2_t h;
-        h[0] = (__bf16)x;
-        h[1] = (__bf16)y;
-        return __builtin_bit_cast(uint32_t, h);
-    }
-};
-
-__device__ __forceinline__ float xor_max(float x, int m) { return fmaxf(x, __shfl_xor(x, m)); }
-
-// Column of key k (0..63) of a block in the LDS copy of V^T: within each 32-key
-// half, key 16u + 4g + j sits at 8g + 4u + j, so the 8 keys a lane feeds to
-// one PV MFMA (4 from each of two S^T tiles) are contiguous.
-__device__ __forceinline__ int vt_col(int k) {
-    const int half = k >> 5, r = k & 31;
-    const int u = r >> 4, g = (r >> 2) & 3, j = r & 3;
-    return 32 * half + 8 * g + 4 * u + j;
-}
-
 template <typename T, int D, bool FUSED, bool LSE>
 __global__ __launch_bounds__(kPrefixThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefix_attn_kernel(
     PrefixParams p, TreeParams tp) {

@@ -134,6 +134,82 @@ __device__ __forceinline__ float group_sum(float x) {
     return x;
 }
 
+// ---------------------------------------------------------------------------
+// v_mfma_f32_16x16x32_{f16,bf16} and the operand layouts the kernels rely on
+// (one wave, lane l, i = l / 16, c = l % 16):
+//   A (16 x 32): lane holds A[c][8i .. 8i+7]      (one 16-byte vector)
+//   B (32 x 16): lane holds B[8i .. 8i+7][c]
+//   D (16 x 16): lane holds D[4i + r][c], r = 0..3
+// ---------------------------------------------------------------------------
+template <typename T>
+struct MfmaOps;
+
+template <>
+struct MfmaOps<F16> {
+    static __device__ __forceinline__ f4_t mma(const Vec16& a, const Vec16& b, f4_t c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8_t, a), __builtin_bit_cast(h8_t, b), c, 0,
+                                                     0, 0);
+    }
+    static __device__ __forceinline__ uint32_t pack2(float x, float y) {
+        h2_t h;
+        h[0] = (_Float16)x;
+        h[1] = (_Float16)y;
+        return __builtin_bit_cast(uint32_t, h);
+    }
+    // the two elements of a packed pair back as fp32
+    static __device__ __forceinline__ float lo(uint32_t w) { return (float)__builtin_bit_cast(h2_t, w)[0]; }
+    static __device__ __forceinline__ float hi(uint32_t w) { return (float)__builtin_bit_cast(h2_t, w)[1]; }
+};
+
+template <>
+struct MfmaOps<BF16> {
+    static __device__ __forceinline__ f4_t mma(const Vec16& a, const Vec16& b, f4_t c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(b8_t, a), __builtin_bit_cast(b8_t, b), c, 0,
+                                                      0, 0);
+    }
+    static __device__ __forceinline__ uint32_t pack2(float x, float y) {
+        b2_t h;
+        h[0] = (__bf16)x;
+        h[1] = (__bf16)y;
+        return __builtin_bit_cast(uint32_t, h);
+    }
+    static __device__ __forceinline__ float lo(uint32_t w) { return __builtin_bit_cast(float, w << 16); }
+    static __device__ __forceinline__ float hi(uint32_t w) { return __builtin_bit_cast(float, w & 0xffff0000u); }
+};
+
+__device__ __forceinline__ float xor_max(float x, int m) { return fmaxf(x, __shfl_xor(x, m)); }
+
+// Reductions over the 4 lanes l, l^16, l^32, l^48 (one MFMA output column)
+// with gfx950's v_permlane16_swap / v_permlane32_swap: swap(x, x) returns the
+// pair (x[l], x[l ^ 16]) (resp. ^ 32) in some order, so op(first, second) is
+// the xor-16 (xor-32) reduction, entirely in VALU.
+__device__ __forceinline__ float col4_max(float x) {
+    auto a = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, x), __builtin_bit_cast(uint32_t, x),
+                                              false, false);
+    x = fmaxf(__builtin_bit_cast(float, (uint32_t)a[0]), __builtin_bit_cast(float, (uint32_t)a[1]));
+    auto b = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, x), __builtin_bit_cast(uint32_t, x),
+                                              false, false);
+    return fmaxf(__builtin_bit_cast(float, (uint32_t)b[0]), __builtin_bit_cast(float, (uint32_t)b[1]));
+}
+__device__ __forceinline__ float col4_sum(float x) {
+    auto a = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, x), __builtin_bit_cast(uint32_t, x),
+                                              false, false);
+    x = __builtin_bit_cast(float, (uint32_t)a[0]) + __builtin_bit_cast(float, (uint32_t)a[1]);
+    auto b = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, x), __builtin_bit_cast(uint32_t, x),
+                                              false, false);
+    return __builtin_bit_cast(float, (uint32_t)b[0]) + __builtin_bit_cast(float, (uint32_t)b[1]);
+}
+
+// Column of key k (0..63) of a block in the LDS copy of V^T: within each 32-key
+// half, key 16u + 4g + j sits at 8g + 4u + j, so the 8 keys a lane feeds to
+// one PV MFMA (4 from each of two S^T tiles) are contiguous.
+__device__ __forceinline__ int vt_col(int k) {
+    const int half = k >> 5, r = k & 31;
+    const int u = r >> 4, g = (r >> 2) & 3, j = r & 3;
+    return 32 * half + 8 * g + 4 * u + j;
+}
+
+
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
 

@@ -1,29 +1,32 @@
 // subtree_stream.hip -- persistent, software-pipelined subtree kernel for the
 // heap ancestor walk (src/ragged_attn.py:262-387 over complete b-ary heaps).
 //
-// The heap parent (i-1)/b makes the ancestors of a subtree a union of
+// Tiling: the heap parent (i-1)/b makes the ancestors of a subtree a union of
 // contiguous BFS level ranges, so the host cuts each tree into tiles (a band
 // of levels under G adjacent roots, plus one ancestor row per level above the
 // band; make_subtree_plan in tree_attn.hip).  Every K/V row of a tile is read
-// from HBM once per kv head, and every ancestor read of every query in the
-// tile is an LDS read.
+// from HBM once per kv head, and every ancestor read is an LDS read.
 //
-// Each workgroup is persistent and walks tiles w, w + gridDim.x, ...  One tile
-// is always in flight: right after tile i is written to LDS, the workgroup
-// computes the metadata of tile i+1 and issues its global loads (K and V rows
-// of the tile, and the Q rows of its queries) into registers, then computes
-// tile i from LDS.  The loads of tile i+1 land while tile i is computed, so
-// HBM sees a steady stream of requests instead of each workgroup's
-// load-wait-compute phases.  Q is staged through LDS with K and V, so the
-// compute phase never waits on global memory; O is written straight from
-// registers.
+// Pipeline: each workgroup is persistent and walks tiles w, w + gridDim.x,
+// ...  Right after tile i is written to LDS, the workgroup issues the global
+// loads of tile i+1 (its K and V rows and the Q rows of its queries) into
+// registers and then computes tile i from LDS, so HBM sees a steady stream of
+// requests.  With a grid that is a multiple of the tile count a workgroup
+// keeps one tile index, and its level table and load addresses are reused.
 //
-// Compute: a query is owned by 8 lanes (4 for D = 32), each owning one
-// contiguous slice of the row (32 bytes at D = 128), so a wave walks 8 queries
-// of one BFS level at a time with a wave-uniform step count; every ancestor
-// step is one LDS row read for K and V, a v_dot2 chain + DPP sum for the score
-// and v_fma_mix for the V accumulation, with a lazily moved softmax
-// reference.  LDS rows are D + 8 elements apart (one 16-byte pad chunk).
+// Compute, on the matrix cores: a tile holds at most 48 (D = 128) or 64 K/V
+// rows and as many queries, so attention over the tile is three small dense
+// products per 16-query block (one wave):
+//   S^T = K Q^T                 v_mfma_f32_16x16x32, keys x queries
+//   mask: a query attends exactly the rows of its ancestor walk (a 64-bit row
+//         mask per query), everything else is -inf
+//   P = exp2(S c - m c), one softmax per query column (max and sum over the
+//       4 lanes holding the column)
+//   O^T = V^T P^T               P split into hi + lo halves of T, so the
+//                               products keep fp32 accuracy in P
+// V stays row-major in LDS like K: the V^T operand of the PV product is read
+// with gfx950's transposing LDS load (ds_read_b64_tr_b16), two per MFMA, in
+// the key order in which the S^T output registers form the P^T operand.
 #include <algorithm>
 
 #include "qattn_common.h"
@@ -33,45 +36,64 @@
 namespace qattn {
 
 constexpr int kStThreads = 256;
-constexpr int kKVPass = 3;    // K/V staging passes per tile (2 vectors each)
-constexpr int kQPass = 3;     // Q staging passes per tile (1 vector each)
-constexpr float kLazy = 8.f;    // softmax reference moves only past 2^kLazy
-constexpr int kCuCache = 256;   // cu_seqlens entries cached in LDS
+constexpr int kCuCache = 256;  // cu_seqlens entries cached in LDS
+// s_waitcnt immediate (gfx9 encoding): vmcnt 0, expcnt and lgkmcnt unconstrained
+constexpr int kWaitVmcnt0 = (7 << 4) | (15 << 8);
+
+// Per-query facts of a tile that depend only on the tile's shape (tile index
+// and sequence length), kept in LDS while a workgroup stays on one tile: the
+// rows the query attends (bit r = K/V row r), its node and q-head offset.
+struct alignas(16) QueryEntry {
+    uint32_t mask_lo, mask_hi;
+    int32_t node, hoff;
+};
 
 template <int D>
 struct StreamGeom {
-    static constexpr int CPR = D / 8;               // 16-byte chunks per row
-    static constexpr int PITCH = D + 8;             // LDS row pitch in elements
-    static constexpr int ROWS_PER_PASS = kStThreads / CPR;
-    static constexpr int KV_ROWS = kKVPass * ROWS_PER_PASS;  // max K/V rows per tile
-    static constexpr int Q_ROWS = kQPass * ROWS_PER_PASS;    // max Q rows per tile
-    static constexpr int LPQ = D >= 64 ? 8 : 4;     // lanes per query
-    static constexpr int NCH = CPR / LPQ;           // 16-byte chunks per lane (contiguous)
-    static constexpr int QPW = 64 / LPQ;            // queries per wave item
+    static constexpr int CPR = D / 8;                 // 16-byte chunks per row
+    static constexpr int RPP = kStThreads / CPR;      // rows per staging pass
+    static constexpr int PASSES = D == 128 ? 3 : (D == 64 ? 2 : 1);
+    static constexpr int KV_ROWS = PASSES * RPP;      // K/V rows per tile (48 or 64)
+    static constexpr int Q_ROWS = KV_ROWS;            // queries per tile
+    static constexpr int PITCH = D + 16;              // K, V and Q row pitch (elements)
+    static constexpr int V_ROWS = 64;                 // V rows the PV product reads (2 x 32 keys)
+    static constexpr int KT = KV_ROWS / 16;           // 16-key tiles of S^T
+    static constexpr int NC = D / 32;                 // 32-element k-chunks of Q K^T
+    static constexpr int ND = D / 16;                 // 16-row d-tiles of O^T
+    static constexpr size_t LDS_BYTES = ((size_t)(KV_ROWS + Q_ROWS + V_ROWS) * PITCH) * 2 +
+                                        (size_t)Q_ROWS * sizeof(QueryEntry) + kCuCache * 4;
 };
 
 // Per-tile state.  Scalars are wave-uniform; first/cnt/off/qb are per lane,
-// lane i describing BFS level lam_min + i.
+// lane i describing BFS level lam_min + i (its first node, node count, LDS row
+// offset = row - node, and first Q row).
 struct TileMeta {
     int32_t valid, tile, seq, kvh, start, n, lo, hi, lam_min, nlev, rows, nq;
     int64_t kvb;
     int32_t first, cnt, off, qb;
 };
 
-// Per-thread source rows of the staging passes of a tile: K/V pass ps reads
-// node (row - offr[ps]); Q pass ps reads query (row - qbl[ps]) of the level
-// whose first node is fl[ps].  Depends only on the level table, so it is
-// reused while a workgroup stays on the same tile; it lives in LDS (each
-// thread reads back only its own entries), not in registers.
-constexpr int kRowMapInts = kKVPass + 2 * kQPass;
-typedef int32_t __attribute__((address_space(3))) * lds_i32_ptr;
+// Source rows of this thread's loads of a tile: K/V pass ps reads node
+// (row - kof[ps]) for row ps * RPP + tid / CPR; Q pass ps reads query
+// (row - qbl[ps]) of the level whose first node is fl[ps].  Depends only on
+// the level table.
+template <int D>
+struct RowMap {
+    int32_t kof[StreamGeom<D>::PASSES], qbl[StreamGeom<D>::PASSES], fl[StreamGeom<D>::PASSES];
+};
+
+template <int D>
+struct Stage {
+    Vec16 k[StreamGeom<D>::PASSES], v[StreamGeom<D>::PASSES], q[StreamGeom<D>::PASSES];
+};
 
 int stream_max_batch() { return kCuCache - 1; }
 
 void stream_tile_caps(int head_dim, int* kv_rows, int* q_rows) {
-    const int rpp = kStThreads / (head_dim / 8);
-    *kv_rows = kKVPass * rpp;
-    *q_rows = kQPass * rpp;
+    const int rows = head_dim == 128 ? StreamGeom<128>::KV_ROWS
+                                     : (head_dim == 64 ? StreamGeom<64>::KV_ROWS : StreamGeom<32>::KV_ROWS);
+    *kv_rows = rows;
+    *q_rows = rows;
 }
 
 // Which tile w is, and its level table (src/ragged_attn.py:376-377 walk:
@@ -206,20 +228,15 @@ __device__ __forceinline__ bool tile_setup(const TreeParams& p, const SubtreePla
     return true;
 }
 
-// Source rows of this thread's staging passes (K/V pass ps covers K/V rows
-// [ps * RPP, (ps + 1) * RPP), Q pass ps Q rows likewise, RPP = rows per pass;
-// thread tid handles chunk tid % CPR of row tid / CPR).
 template <int D>
-__device__ __forceinline__ void tile_rowmap(const TileMeta& t, lds_i32_ptr rmap) {
+__device__ __forceinline__ void tile_rowmap(const TileMeta& t, RowMap<D>& rm) {
     using Geo = StreamGeom<D>;
-    const int rsub = threadIdx.x / Geo::CPR;
-    struct {
-        int32_t offr[kKVPass], qbl[kQPass], fl[kQPass];
-    } rm;
+    const int tid = threadIdx.x;
+    const int rsub = tid / Geo::CPR;
+    const int o0 = rl(t.off, 0);
 #pragma unroll
-    for (int ps = 0; ps < kKVPass; ++ps) rm.offr[ps] = rl(t.off, 0);
-#pragma unroll
-    for (int ps = 0; ps < kQPass; ++ps) {
+    for (int ps = 0; ps < Geo::PASSES; ++ps) {
+        rm.kof[ps] = o0;
         rm.qbl[ps] = 0;
         rm.fl[ps] = 0;
     }
@@ -229,282 +246,339 @@ __device__ __forceinline__ void tile_rowmap(const TileMeta& t, lds_i32_ptr rmap)
         const int oi = rl(t.off, i), fi = rl(t.first, i);
         const int bi = oi + fi, qi = rl(t.qb, i);
 #pragma unroll
-        for (int ps = 0; ps < kKVPass; ++ps) {
-            if (ps * Geo::ROWS_PER_PASS + rsub >= bi) rm.offr[ps] = oi;
+        for (int ps = 0; ps < Geo::PASSES; ++ps) {
+            if (ps * Geo::RPP + rsub >= bi) rm.kof[ps] = oi;
         }
         if (t.lam_min + i >= t.lo) {
 #pragma unroll
-            for (int ps = 0; ps < kQPass; ++ps) {
-                if (ps * Geo::ROWS_PER_PASS + rsub >= qi) {
+            for (int ps = 0; ps < Geo::PASSES; ++ps) {
+                if (ps * Geo::RPP + rsub >= qi) {
                     rm.qbl[ps] = qi;
                     rm.fl[ps] = fi;
                 }
             }
         }
     }
-    const int tid = threadIdx.x;
-#pragma unroll
-    for (int ps = 0; ps < kKVPass; ++ps) rmap[ps * kStThreads + tid] = rm.offr[ps];
-#pragma unroll
-    for (int ps = 0; ps < kQPass; ++ps) {
-        rmap[(kKVPass + ps) * kStThreads + tid] = rm.qbl[ps];
-        rmap[(kKVPass + kQPass + ps) * kStThreads + tid] = rm.fl[ps];
-    }
 }
 
 // Issue the global loads of a tile into the staging registers.
 template <int D>
 __device__ __forceinline__ void tile_issue(const TreeParams& p, const Divider& gdiv, const TileMeta& t,
-                                           lds_i32_ptr rmap, Vec16 (&kv)[kKVPass][2], Vec16 (&qv)[kQPass]) {
+                                           const RowMap<D>& rm, Stage<D>& sg) {
     using Geo = StreamGeom<D>;
     const int tid = threadIdx.x;
     const int rsub = tid / Geo::CPR, c = tid % Geo::CPR;
     const uint16_t* kg = (const uint16_t*)p.k + (int64_t)t.kvh * p.sk_h + 8 * c;
     const uint16_t* vg = (const uint16_t*)p.v + (int64_t)t.kvh * p.sv_h + 8 * c;
 #pragma unroll
-    for (int ps = 0; ps < kKVPass; ++ps) {
-        if (ps * Geo::ROWS_PER_PASS >= t.rows) break;  // wave-uniform
-        const int r = ps * Geo::ROWS_PER_PASS + rsub;
+    for (int ps = 0; ps < Geo::PASSES; ++ps) {
+        if (ps * Geo::RPP >= t.rows) break;  // wave-uniform
+        const int r = ps * Geo::RPP + rsub;
         if (r < t.rows) {
-            const int64_t row = t.kvb + (r - rmap[ps * kStThreads + tid]);
-            kv[ps][0] = ld16(kg + row * p.sk_t);
-            kv[ps][1] = ld16(vg + row * p.sv_t);
+            const int64_t row = t.kvb + (r - rm.kof[ps]);
+            sg.k[ps] = ld16(kg + row * p.sk_t);
+            sg.v[ps] = ld16(vg + row * p.sv_t);
         }
     }
     const int g = p.group;
 #pragma unroll
-    for (int ps = 0; ps < kQPass; ++ps) {
-        if (ps * Geo::ROWS_PER_PASS >= t.nq) break;  // wave-uniform
-        const int q = ps * Geo::ROWS_PER_PASS + rsub;
+    for (int ps = 0; ps < Geo::PASSES; ++ps) {
+        if (ps * Geo::RPP >= t.nq) break;  // wave-uniform
+        const int q = ps * Geo::RPP + rsub;
         if (q < t.nq) {
-            const int sq = q - rmap[(kKVPass + ps) * kStThreads + tid];
+            const int sq = q - rm.qbl[ps];
             const int nd = divide(sq, gdiv);
-            const int node = rmap[(kKVPass + kQPass + ps) * kStThreads + tid] + nd;
+            const int node = rm.fl[ps] + nd;
             const int head = t.kvh * g + (sq - nd * g);
-            qv[ps] = ld16((const uint16_t*)p.q + ((int64_t)t.start + node) * p.sq_t + (int64_t)head * p.sq_h + 8 * c);
+            sg.q[ps] = ld16((const uint16_t*)p.q + ((int64_t)t.start + node) * p.sq_t + (int64_t)head * p.sq_h + 8 * c);
         }
     }
 }
 
+// Write the staged tile to LDS (K, V and Q rows at the padded pitch).  V rows
+// past the tile's last row keep the previous tile's (finite) values or the
+// zeros written at kernel start; P = 0 multiplies them.
 template <int D>
 __device__ __forceinline__ void tile_store(const TileMeta& t, uint16_t* Ks, uint16_t* Vs, uint16_t* Qs,
-                                           const Vec16 (&kv)[kKVPass][2], const Vec16 (&qv)[kQPass]) {
+                                           const Stage<D>& sg) {
     using Geo = StreamGeom<D>;
     const int tid = threadIdx.x;
     const int rsub = tid / Geo::CPR, c = tid % Geo::CPR;
 #pragma unroll
-    for (int ps = 0; ps < kKVPass; ++ps) {
-        if (ps * Geo::ROWS_PER_PASS >= t.rows) break;
-        const int r = ps * Geo::ROWS_PER_PASS + rsub;
+    for (int ps = 0; ps < Geo::PASSES; ++ps) {
+        if (ps * Geo::RPP >= t.rows) break;
+        const int r = ps * Geo::RPP + rsub;
         if (r < t.rows) {
-            st16(Ks + r * Geo::PITCH + 8 * c, kv[ps][0]);
-            st16(Vs + r * Geo::PITCH + 8 * c, kv[ps][1]);
+            st16(Ks + r * Geo::PITCH + 8 * c, sg.k[ps]);
+            st16(Vs + r * Geo::PITCH + 8 * c, sg.v[ps]);
         }
     }
 #pragma unroll
-    for (int ps = 0; ps < kQPass; ++ps) {
-        if (ps * Geo::ROWS_PER_PASS >= t.nq) break;
-        const int q = ps * Geo::ROWS_PER_PASS + rsub;
-        if (q < t.nq) st16(Qs + q * Geo::PITCH + 8 * c, qv[ps]);
+    for (int ps = 0; ps < Geo::PASSES; ++ps) {
+        if (ps * Geo::RPP >= t.nq) break;
+        const int q = ps * Geo::RPP + rsub;
+        if (q < t.nq) st16(Qs + q * Geo::PITCH + 8 * c, sg.q[ps]);
     }
 }
 
-// q . k of one query against one LDS row (lane j of the query's LPQ lanes
-// owns elements [8 NCH j, 8 NCH (j+1)) of every row): one dependent chain of
-// v_dot2 per lane, then a DPP sum over the query's lanes.
-template <typename T, int NCH, int LPQ>
-__device__ __forceinline__ float qk_row(const Vec16* qf, const Vec16* kf) {
-    float d = dot2<T>(qf[0].w[0], kf[0].w[0], 0.f);
-#pragma unroll
-    for (int i = 0; i < NCH; ++i) {
-#pragma unroll
-        for (int w = (i == 0 ? 1 : 0); w < 4; ++w) d = dot2<T>(qf[i].w[w], kf[i].w[w], d);
-    }
-    return group_sum<LPQ>(d);
+// Four 16-bit elements of V^T through the transposing LDS load: within each
+// 16-lane group, lane j reads V[key0 + j / 4][d0 + 4 (j % 4) .. +3] and lane
+// i receives V[key0 + k][d0 + i] for k = 0..3.
+__device__ __forceinline__ uint2 vt_read4(const uint16_t* Vs, int pitch, int key0, int d0, int j) {
+    typedef short v4s __attribute__((ext_vector_type(4)));
+    const uint16_t* a = Vs + (key0 + (j >> 2)) * pitch + d0 + 4 * (j & 3);
+    const v4s r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s*)a);
+    return __builtin_bit_cast(uint2, r);
 }
 
-// Initial state from split-K prefix partials, contiguous lane layout (lane j
-// of a query owns elements [8 NCH j, 8 NCH (j+1))).
-template <int D>
-__device__ __forceinline__ void load_partial_state_c(const TreeParams& p, int64_t qrow, int h, int j, float& m,
-                                                     float& l, float* acc) {
-    constexpr int NCH = StreamGeom<D>::NCH;
-    const int64_t plane = p.total_tokens * (int64_t)p.Hq;
-    const int64_t idx = qrow * p.Hq + h;
-    float m0 = -INFINITY;
-    for (int s = 0; s < p.n_split; ++s) m0 = fmaxf(m0, p.part_m[s * plane + idx]);
-    m = m0;
-    l = 0.f;
+// Build the query table of a tile: thread q handles query q.  The walk
+// (src/ragged_attn.py:338-377) attends steps t = 0..min(level, max_depth),
+// levels level - t, exactly the steps with c_t != c_{t-1}; the level loop runs
+// from the deepest level up so every level offset is a wave-uniform readlane.
+__device__ __forceinline__ void build_query_table(const TreeParams& p, const Divider& gdiv, const TileMeta& t,
+                                                  QueryEntry* qt) {
+    const int g = p.group;
+    for (int q0 = 0; q0 < t.nq; q0 += kStThreads) {
+        const int q = q0 + (int)threadIdx.x;
+        int li = -1, qbl = 0, fi = 0;
+        for (int i = 0; i < t.nlev; ++i) {
+            const int qi = rl(t.qb, i), ci = rl(t.cnt, i) * g, f = rl(t.first, i);
+            if (t.lam_min + i >= t.lo && q >= qi && q < qi + ci) {
+                li = i;
+                qbl = qi;
+                fi = f;
+            }
+        }
+        const int s_in = q - qbl;
+        const int nd = divide(s_in, gdiv);
+        const int node = fi + nd;
+        const int lam = t.lam_min + li;
+        int steps = li >= 0 ? (lam < p.max_depth ? lam : p.max_depth) + 1 : 0;
+        uint64_t mask = 0;
+        int32_t cur = node;
+        int lv = li;
+        for (int i = t.nlev - 1; i >= 0; --i) {
+            const int oi = rl(t.off, i);
+            if (lv == i && steps > 0) {
+                mask |= uint64_t(1) << (cur + oi);
+                cur = heap_parent(cur, p.bdiv);
+                --lv;
+                --steps;
+            }
+        }
+        if (q < t.nq) qt[q] = QueryEntry{(uint32_t)mask, (uint32_t)(mask >> 32), node, s_in - nd * g};
+    }
+}
+
+// One wave: attention of 16 queries (query block qb) of the tile held in LDS.
+template <typename T, int D, bool LSE, bool PSTATE>
+__device__ __forceinline__ void block_compute(const TreeParams& p, const TileMeta& t, int qb, const uint16_t* Ks,
+                                              const uint16_t* Vs, const uint16_t* Qs, const QueryEntry* qt) {
+    using Geo = StreamGeom<D>;
+    constexpr int NC = Geo::NC, ND = Geo::ND, KT = Geo::KT;
+    const int lane = threadIdx.x & 63;
+    const int c16 = lane & 15, i4 = lane >> 4;
+    const int g = p.group;
+
+    // ---- this lane's query (column c16 of the block) ----
+    const int sq = 16 * qb + c16;
+    const bool qvalid = sq < t.nq;
+    QueryEntry qe = QueryEntry{0u, 0u, 0, 0};
+    if (qvalid) qe = qt[sq];
+    const uint64_t mask = ((uint64_t)qe.mask_hi << 32) | qe.mask_lo;
+    const int64_t qrow = (int64_t)t.start + qe.node;
+    const int qh = t.kvh * g + qe.hoff;
+
+    // ---- S^T = K Q^T ----
+    Vec16 qf[NC];
 #pragma unroll
-    for (int e = 0; e < 8 * NCH; ++e) acc[e] = 0.f;
-    if (m0 == -INFINITY) return;
-    for (int s = 0; s < p.n_split; ++s) {
-        const float ms = p.part_m[s * plane + idx];
-        if (ms == -INFINITY) continue;
-        const float w = fast_exp2(ms - m0);
-        l = __builtin_fmaf(w, p.part_l[s * plane + idx], l);
-        const float* a = p.part_acc + (s * plane + idx) * D + 8 * NCH * j;
+    for (int kc = 0; kc < NC; ++kc) qf[kc] = ld16(Qs + (16 * qb + c16) * Geo::PITCH + 32 * kc + 8 * i4);
+    const int kt_used = (t.rows + 15) / 16;
+    f4_t sacc[KT];
 #pragma unroll
-        for (int e = 0; e < 8 * NCH; e += 4) {
-            const float4 v = *reinterpret_cast<const float4*>(a + e);
-            acc[e] = __builtin_fmaf(w, v.x, acc[e]);
-            acc[e + 1] = __builtin_fmaf(w, v.y, acc[e + 1]);
-            acc[e + 2] = __builtin_fmaf(w, v.z, acc[e + 2]);
-            acc[e + 3] = __builtin_fmaf(w, v.w, acc[e + 3]);
+    for (int kt = 0; kt < KT; ++kt) {
+        sacc[kt] = f4_t{0.f, 0.f, 0.f, 0.f};
+        if (kt < kt_used) {  // wave-uniform
+#pragma unroll
+            for (int kc = 0; kc < NC; ++kc) {
+                const Vec16 a = ld16(Ks + (16 * kt + c16) * Geo::PITCH + 32 * kc + 8 * i4);
+                sacc[kt] = MfmaOps<T>::mma(a, qf[kc], sacc[kt]);
+            }
         }
     }
-}
 
-// Normalise and store one query's output, contiguous lane layout (+ LSE).
-template <typename T, int D, bool LSE>
-__device__ __forceinline__ void write_out_c(const TreeParams& p, int64_t qrow, int h, int j, float m, float l,
-                                            float* acc) {
-    constexpr int NCH = StreamGeom<D>::NCH;
+    // ---- masked softmax per query column ----
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt) {
+        const uint32_t bits = (uint32_t)(mask >> (16 * kt + 4 * i4)) & 15u;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const float s = ((bits >> r) & 1u) ? sacc[kt][r] : -INFINITY;
+            sacc[kt][r] = s;
+            mx = fmaxf(mx, s);
+        }
+    }
+    mx = col4_max(mx);
+    const float c = p.scale_log2;
+    float mref = (mx == -INFINITY) ? 0.f : mx * c;  // a query with no row (invalid column)
+    // Split-K prefix partial states (flash-decoding merge): the reference
+    // becomes max(tree max, prefix max) and the accumulators start from the
+    // prefix states weighted by 2^(m_s - reference), one split at a time.
+    float lpre = 0.f;
+    f4_t oacc[ND];
+#pragma unroll
+    for (int dt = 0; dt < ND; ++dt) oacc[dt] = f4_t{0.f, 0.f, 0.f, 0.f};
+    if constexpr (PSTATE) {
+        if (qvalid) {
+            const int64_t plane = p.total_tokens * (int64_t)p.Hq;
+            const int64_t idx = qrow * p.Hq + qh;
+            float mp = -INFINITY;
+            for (int s = 0; s < p.n_split; ++s) mp = fmaxf(mp, p.part_m[s * plane + idx]);
+            if (mp != -INFINITY) {
+                mref = fmaxf(mref, mp);
+                for (int s = 0; s < p.n_split; ++s) {
+                    const float ms = p.part_m[s * plane + idx];
+                    if (ms == -INFINITY) continue;
+                    const float w = fast_exp2(ms - mref);
+                    lpre = __builtin_fmaf(w, p.part_l[s * plane + idx], lpre);
+                    const float* a = p.part_acc + (s * plane + idx) * D + 4 * i4;
+#pragma unroll
+                    for (int dt = 0; dt < ND; ++dt) {
+                        const float4 v = *reinterpret_cast<const float4*>(a + 16 * dt);
+                        oacc[dt][0] = __builtin_fmaf(w, v.x, oacc[dt][0]);
+                        oacc[dt][1] = __builtin_fmaf(w, v.y, oacc[dt][1]);
+                        oacc[dt][2] = __builtin_fmaf(w, v.z, oacc[dt][2]);
+                        oacc[dt][3] = __builtin_fmaf(w, v.w, oacc[dt][3]);
+                    }
+                }
+            }
+        }
+    }
+    const float mc = mref;
+    float ls = 0.f;
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const float e = fast_exp2(__builtin_fmaf(sacc[kt][r], c, -mc));  // -inf -> 0
+            sacc[kt][r] = e;
+            ls += e;
+        }
+    }
+    ls = col4_sum(ls);
+
+    // ---- O^T = V^T P^T, P = hi + lo in T ----
+    Vec16 phi[2], plo[2];
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int kt = 2 * kk + h;
+            float pv[4] = {0.f, 0.f, 0.f, 0.f};
+            if (kt < KT) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) pv[r] = sacc[kt][r];
+            }
+            const uint32_t h01 = MfmaOps<T>::pack2(pv[0], pv[1]);
+            const uint32_t h23 = MfmaOps<T>::pack2(pv[2], pv[3]);
+            phi[kk].w[2 * h] = h01;
+            phi[kk].w[2 * h + 1] = h23;
+            plo[kk].w[2 * h] = MfmaOps<T>::pack2(pv[0] - MfmaOps<T>::lo(h01), pv[1] - MfmaOps<T>::hi(h01));
+            plo[kk].w[2 * h + 1] = MfmaOps<T>::pack2(pv[2] - MfmaOps<T>::lo(h23), pv[3] - MfmaOps<T>::hi(h23));
+        }
+    }
+    const int kk_used = (t.rows + 31) / 32;
+#pragma unroll
+    for (int dt = 0; dt < ND; ++dt) {
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+            if (kk < kk_used) {  // wave-uniform
+                // A[d][e]: e = 0..3 -> key 32 kk + 4 i4 + e, e = 4..7 -> key 32 kk + 16 + 4 i4 + (e - 4)
+                const uint2 a0 = vt_read4(Vs, Geo::PITCH, 32 * kk + 4 * i4, 16 * dt, c16);
+                const uint2 a1 = vt_read4(Vs, Geo::PITCH, 32 * kk + 16 + 4 * i4, 16 * dt, c16);
+                const Vec16 a = Vec16{{a0.x, a0.y, a1.x, a1.y}};
+                oacc[dt] = MfmaOps<T>::mma(a, phi[kk], oacc[dt]);
+                oacc[dt] = MfmaOps<T>::mma(a, plo[kk], oacc[dt]);
+            }
+        }
+    }
+
+    // ---- normalise ----
+    const float m = mc, l = ls + lpre;
     const float l_safe = (l == 0.f) ? 1.f : l;  // src/ragged_attn.py:379-380
     const float inv = __builtin_amdgcn_rcpf(l_safe);
-    uint16_t* optr = (uint16_t*)p.o + qrow * p.so_t + (int64_t)h * p.so_h + 8 * NCH * j;
-#pragma unroll
-    for (int i = 0; i < NCH; ++i) {
-        float r[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) r[e] = acc[8 * i + e] * inv;
-        st16(optr + 8 * i, pack8<T>(r));
-    }
     if constexpr (LSE) {
-        if (j == 0) p.lse[qrow * p.slse_t + (int64_t)h * p.slse_h] = (m + fast_log2(l_safe)) * kLn2;
+        if (qvalid && i4 == 0) p.lse[qrow * p.slse_t + (int64_t)qh * p.slse_h] = (m + fast_log2(l_safe)) * kLn2;
+    }
+
+    // ---- O: lane holds O^T[16 dt + 4 i4 + r][c16], stored straight as 8-byte
+    // pieces; the 4 lanes of a column fill 32 contiguous bytes per d-tile and
+    // the d-tiles complete the row in L2 ----
+    if (qvalid) {
+        uint16_t* optr = (uint16_t*)p.o + qrow * p.so_t + (int64_t)qh * p.so_h + 4 * i4;
+#pragma unroll
+        for (int dt = 0; dt < ND; ++dt) {
+            *reinterpret_cast<uint2*>(optr + 16 * dt) =
+                make_uint2(MfmaOps<T>::pack2(oacc[dt][0] * inv, oacc[dt][1] * inv),
+                           MfmaOps<T>::pack2(oacc[dt][2] * inv, oacc[dt][3] * inv));
+        }
     }
 }
 
 template <typename T, int D, bool LSE, bool PSTATE>
-__device__ __forceinline__ void tile_compute(const TreeParams& p, const Divider& gdiv, const TileMeta& t,
-                                             const uint16_t* Ks, const uint16_t* Vs, const uint16_t* Qs) {
-    using Geo = StreamGeom<D>;
-    constexpr int NCH = Geo::NCH, LPQ = Geo::LPQ, QPW = Geo::QPW;
-    const int lane64 = threadIdx.x & 63;
+__device__ __forceinline__ void tile_compute(const TreeParams& p, const TileMeta& t, const uint16_t* Ks,
+                                             const uint16_t* Vs, const uint16_t* Qs, const QueryEntry* qt) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int grp = lane64 / LPQ, j = lane64 % LPQ;
-    const int g = p.group;
-    // wave items: QPW (node, q head) pairs of one level; item k of level L
-    const int lam_l = t.lam_min + lane64;
-    const int nw = (lane64 < t.nlev && lam_l >= t.lo) ? (t.cnt * g + QPW - 1) / QPW : 0;
-    int L = t.lo, k = wave;
-    for (;;) {
-        while (L <= t.hi) {
-            const int w = rl(nw, L - t.lam_min);
-            if (k < w) break;
-            k -= w;
-            ++L;
-        }
-        if (L > t.hi) break;
-        const int li = L - t.lam_min;
-        const int s = k * QPW + grp;
-        if (s < rl(t.cnt, li) * g) {
-            const int nd = divide(s, gdiv);
-            const int node = rl(t.first, li) + nd;
-            const int qh = t.kvh * g + (s - nd * g);
-            const int64_t qrow = (int64_t)t.start + node;
-            Vec16 qf[NCH];
-            const uint16_t* qs = Qs + (rl(t.qb, li) + s) * Geo::PITCH + 8 * NCH * j;
-#pragma unroll
-            for (int i = 0; i < NCH; ++i) qf[i] = ld16(qs + 8 * i);
-            // steps t = 0..min(L, max_depth) attend levels L - t: the heap walk
-            // strictly decreases until the root, so these are exactly the
-            // steps with c_t != c_{t-1} (src/ragged_attn.py:338-377).
-            const int nsteps = (L < p.max_depth ? L : p.max_depth) + 1;
-            const float c = p.scale_log2;
-            int32_t cur = node;
-            int lv = li;  // level index (lane of the level table) of cur
-            float m, l, acc[8 * NCH];
-            int t0 = 0;
-            if constexpr (PSTATE) {
-                load_partial_state_c<D>(p, qrow, qh, j, m, l, acc);
-            } else {
-                // step 0, the query's own row, sets the reference: p = 1
-                const int row = (cur + rl(t.off, lv)) * Geo::PITCH + 8 * NCH * j;
-                Vec16 kf[NCH], vf[NCH];
-#pragma unroll
-                for (int i = 0; i < NCH; ++i) {
-                    kf[i] = ld16(Ks + row + 8 * i);
-                    vf[i] = ld16(Vs + row + 8 * i);
-                }
-                m = qk_row<T, NCH, LPQ>(qf, kf) * c;
-                l = 1.f;
-#pragma unroll
-                for (int i = 0; i < NCH; ++i) {
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) acc[8 * i + e] = elem<T>(vf[i], e);
-                }
-                cur = heap_parent(cur, p.bdiv);
-                --lv;
-                t0 = 1;
-            }
-            // Lazy rescaling: the reference m moves only when a score exceeds
-            // it by more than kLazy (log2 units), so P <= 2^kLazy and the
-            // accumulators are rescaled on few steps; l shares the reference,
-            // so o = acc / l and lse = m + log2(l) are unchanged.
-            for (int st = t0; st < nsteps; ++st) {
-                const int row = (cur + rl(t.off, lv)) * Geo::PITCH + 8 * NCH * j;
-                Vec16 kf[NCH], vf[NCH];
-#pragma unroll
-                for (int i = 0; i < NCH; ++i) {
-                    kf[i] = ld16(Ks + row + 8 * i);
-                    vf[i] = ld16(Vs + row + 8 * i);
-                }
-                const float sc = qk_row<T, NCH, LPQ>(qf, kf) * c;
-                const bool move = sc > m + kLazy;
-                if (__builtin_expect(__any(move), 0)) {
-                    const float m_new = move ? sc : m;
-                    const float alpha = fast_exp2(m - m_new);  // m = -inf (empty state): 0
-                    l *= alpha;
-#pragma unroll
-                    for (int e = 0; e < 8 * NCH; ++e) acc[e] *= alpha;
-                    m = m_new;
-                }
-                const float pt = fast_exp2(sc - m);
-                l += pt;
-#pragma unroll
-                for (int i = 0; i < NCH; ++i) axpy8<T>(acc + 8 * i, pt, vf[i]);
-                cur = heap_parent(cur, p.bdiv);
-                --lv;
-            }
-            write_out_c<T, D, LSE>(p, qrow, qh, j, m, l, acc);
-        }
-        k += kStThreads / 64;
-    }
+    for (int qb = wave; 16 * qb < t.nq; qb += kStThreads / 64)
+        block_compute<T, D, LSE, PSTATE>(p, t, qb, Ks, Vs, Qs, qt);
 }
 
 // The staging registers of one tile stay live across the compute phase of the
-// previous one; 3 workgroups of 256 threads per CU (about 49 KB of LDS each)
+// previous one; 3 workgroups of 256 threads per CU (about 50 KB of LDS each)
 // need at most 168 VGPRs.
 template <typename T, int D, bool LSE, bool PSTATE>
-__global__ __launch_bounds__(kStThreads) __attribute__((amdgpu_waves_per_eu(3, 3))) void tree_stream_kernel(
+__global__ __launch_bounds__(kStThreads)
+__attribute__((amdgpu_waves_per_eu(3, 3))) void tree_stream_kernel(
     TreeParams p, SubtreePlan plan, StreamArgs sa) {
     using Geo = StreamGeom<D>;
     extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
     uint16_t* Ks = smem;
-    uint16_t* Vs = Ks + Geo::KV_ROWS * Geo::PITCH;
-    uint16_t* Qs = Vs + Geo::KV_ROWS * Geo::PITCH;
-    int32_t* cuc = reinterpret_cast<int32_t*>(Qs + Geo::Q_ROWS * Geo::PITCH);
-    const lds_i32_ptr rmap = (lds_i32_ptr)(cuc + kCuCache);
+    uint16_t* Qs = Ks + Geo::KV_ROWS * Geo::PITCH;
+    uint16_t* Vs = Qs + Geo::Q_ROWS * Geo::PITCH;
+    QueryEntry* qtab = reinterpret_cast<QueryEntry*>(Vs + Geo::V_ROWS * Geo::PITCH);
+    int32_t* cuc = reinterpret_cast<int32_t*>(qtab + Geo::Q_ROWS);
     const Divider gdiv = sa.gdiv;
 
     int w = blockIdx.x;
     if (w >= sa.n_work) return;  // uniform: no barrier below is skipped by a subset of waves
     for (int i = threadIdx.x; i <= p.B; i += kStThreads) cuc[i] = p.cu[i];  // p.B < kCuCache
+    // V rows the PV product reads but no tile has written yet must hold finite
+    // values (P = 0 multiplies them): zero them once
+    for (int i = threadIdx.x; i < Geo::V_ROWS * Geo::PITCH / 8; i += kStThreads)
+        st16(Vs + 8 * i, Vec16{{0u, 0u, 0u, 0u}});
     __syncthreads();
     const int32_t __attribute__((address_space(3)))* cu_lds =
         (const int32_t __attribute__((address_space(3)))*)cuc;
 
     TileMeta cur, none;
     none.valid = 0;
+    int tab_tile = -1, tab_n = -1;  // shape the query table was built for
+    RowMap<D> rm;
+    Stage<D> sg;
     tile_setup<D>(p, plan, sa, cu_lds, w, none, cur);
-    Vec16 kv[kKVPass][2], qv[kQPass];
     if (cur.valid) {
-        tile_rowmap<D>(cur, rmap);
-        tile_issue<D>(p, gdiv, cur, rmap, kv, qv);
+        tile_rowmap<D>(cur, rm);
+        tile_issue<D>(p, gdiv, cur, rm, sg);
     }
     for (;;) {
-        if (cur.valid) tile_store<D>(cur, Ks, Vs, Qs, kv, qv);
+        // The staged loads must have landed before they are written to LDS;
+        // waiting for all vector memory here (the previous tile's O stores
+        // have had a whole compute phase to drain) also means no path leaves
+        // a load pending into the issue code below, which would otherwise get
+        // a conservative wait on every outstanding store.
+        __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+        if (cur.valid) tile_store<D>(cur, Ks, Vs, Qs, sg);
         __syncthreads();
         const int wn = w + gridDim.x;
         const bool more = wn < sa.n_work;
@@ -512,11 +586,20 @@ __global__ __launch_bounds__(kStThreads) __attribute__((amdgpu_waves_per_eu(3, 3
         if (more) {
             const bool fresh = tile_setup<D>(p, plan, sa, cu_lds, wn, cur, nxt);
             if (nxt.valid) {
-                if (fresh) tile_rowmap<D>(nxt, rmap);
-                tile_issue<D>(p, gdiv, nxt, rmap, kv, qv);
+                if (fresh) tile_rowmap<D>(nxt, rm);
+                tile_issue<D>(p, gdiv, nxt, rm, sg);
             }
         }
-        if (cur.valid) tile_compute<T, D, LSE, PSTATE>(p, gdiv, cur, Ks, Vs, Qs);
+        if (cur.valid) {
+            // the query table follows the tile shape (uniform branch)
+            if (cur.tile != tab_tile || cur.n != tab_n) {
+                build_query_table(p, gdiv, cur, qtab);
+                tab_tile = cur.tile;
+                tab_n = cur.n;
+                __syncthreads();
+            }
+            tile_compute<T, D, LSE, PSTATE>(p, cur, Ks, Vs, Qs, qtab);
+        }
         __syncthreads();
         if (!more) break;
         cur = nxt;
@@ -537,8 +620,7 @@ static int launch_stream_t(const TreeParams& p, const SubtreePlan& plan, hipStre
         set_error("subtree kernel: batch %d exceeds %d sequences", p.B, kCuCache - 1);
         return QATTN_ERR_ARG;
     }
-    const size_t lds = ((size_t)2 * Geo::KV_ROWS + Geo::Q_ROWS) * Geo::PITCH * 2 + kCuCache * 4 +
-                       (size_t)kRowMapInts * kStThreads * 4;
+    const size_t lds = Geo::LDS_BYTES;
     auto kern = tree_stream_kernel<T, D, LSE, PSTATE>;
     int dev = 0, cus = 0, per_cu = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
