@@ -73,13 +73,13 @@ struct TileMeta {
     int32_t first, cnt, off, qb;
 };
 
-// Source rows of this thread's loads of a tile: K/V pass ps reads node
-// (row - kof[ps]) for row ps * RPP + tid / CPR; Q pass ps reads query
-// (row - qbl[ps]) of the level whose first node is fl[ps].  Depends only on
-// the level table.
+// Element offsets of this thread's loads of a tile, relative to the tile's
+// K, V and Q base addresses: K/V pass ps reads LDS row ps * RPP + tid / CPR,
+// Q pass ps Q row ps * RPP + tid / CPR (chunk tid % CPR).  They depend only on
+// the level table, so a workgroup that stays on one tile computes them once.
 template <int D>
 struct RowMap {
-    int32_t kof[StreamGeom<D>::PASSES], qbl[StreamGeom<D>::PASSES], fl[StreamGeom<D>::PASSES];
+    int64_t koff[StreamGeom<D>::PASSES], voff[StreamGeom<D>::PASSES], qoff[StreamGeom<D>::PASSES];
 };
 
 template <int D>
@@ -229,16 +229,18 @@ __device__ __forceinline__ bool tile_setup(const TreeParams& p, const SubtreePla
 }
 
 template <int D>
-__device__ __forceinline__ void tile_rowmap(const TileMeta& t, RowMap<D>& rm) {
+__device__ __forceinline__ void tile_rowmap(const TreeParams& p, const Divider& gdiv, const TileMeta& t,
+                                            RowMap<D>& rm) {
     using Geo = StreamGeom<D>;
     const int tid = threadIdx.x;
-    const int rsub = tid / Geo::CPR;
+    const int rsub = tid / Geo::CPR, c = tid % Geo::CPR;
+    int kof[Geo::PASSES], qbl[Geo::PASSES], fl[Geo::PASSES];
     const int o0 = rl(t.off, 0);
 #pragma unroll
     for (int ps = 0; ps < Geo::PASSES; ++ps) {
-        rm.kof[ps] = o0;
-        rm.qbl[ps] = 0;
-        rm.fl[ps] = 0;
+        kof[ps] = o0;
+        qbl[ps] = 0;
+        fl[ps] = 0;
     }
     for (int i = 0; i < t.nlev; ++i) {
         const int ci = rl(t.cnt, i);
@@ -247,51 +249,51 @@ __device__ __forceinline__ void tile_rowmap(const TileMeta& t, RowMap<D>& rm) {
         const int bi = oi + fi, qi = rl(t.qb, i);
 #pragma unroll
         for (int ps = 0; ps < Geo::PASSES; ++ps) {
-            if (ps * Geo::RPP + rsub >= bi) rm.kof[ps] = oi;
+            if (ps * Geo::RPP + rsub >= bi) kof[ps] = oi;
         }
         if (t.lam_min + i >= t.lo) {
 #pragma unroll
             for (int ps = 0; ps < Geo::PASSES; ++ps) {
                 if (ps * Geo::RPP + rsub >= qi) {
-                    rm.qbl[ps] = qi;
-                    rm.fl[ps] = fi;
+                    qbl[ps] = qi;
+                    fl[ps] = fi;
                 }
             }
-        }
-    }
-}
-
-// Issue the global loads of a tile into the staging registers.
-template <int D>
-__device__ __forceinline__ void tile_issue(const TreeParams& p, const Divider& gdiv, const TileMeta& t,
-                                           const RowMap<D>& rm, Stage<D>& sg) {
-    using Geo = StreamGeom<D>;
-    const int tid = threadIdx.x;
-    const int rsub = tid / Geo::CPR, c = tid % Geo::CPR;
-    const uint16_t* kg = (const uint16_t*)p.k + (int64_t)t.kvh * p.sk_h + 8 * c;
-    const uint16_t* vg = (const uint16_t*)p.v + (int64_t)t.kvh * p.sv_h + 8 * c;
-#pragma unroll
-    for (int ps = 0; ps < Geo::PASSES; ++ps) {
-        if (ps * Geo::RPP >= t.rows) break;  // wave-uniform
-        const int r = ps * Geo::RPP + rsub;
-        if (r < t.rows) {
-            const int64_t row = t.kvb + (r - rm.kof[ps]);
-            sg.k[ps] = ld16(kg + row * p.sk_t);
-            sg.v[ps] = ld16(vg + row * p.sv_t);
         }
     }
     const int g = p.group;
 #pragma unroll
     for (int ps = 0; ps < Geo::PASSES; ++ps) {
-        if (ps * Geo::RPP >= t.nq) break;  // wave-uniform
-        const int q = ps * Geo::RPP + rsub;
-        if (q < t.nq) {
-            const int sq = q - rm.qbl[ps];
-            const int nd = divide(sq, gdiv);
-            const int node = rm.fl[ps] + nd;
-            const int head = t.kvh * g + (sq - nd * g);
-            sg.q[ps] = ld16((const uint16_t*)p.q + ((int64_t)t.start + node) * p.sq_t + (int64_t)head * p.sq_h + 8 * c);
+        const int64_t node = ps * Geo::RPP + rsub - kof[ps];  // K/V row relative to the tile's kv base
+        rm.koff[ps] = node * p.sk_t + 8 * c;
+        rm.voff[ps] = node * p.sv_t + 8 * c;
+        const int sq = ps * Geo::RPP + rsub - qbl[ps];
+        const int nd = divide(sq, gdiv);
+        rm.qoff[ps] = (int64_t)(fl[ps] + nd) * p.sq_t + (int64_t)(sq - nd * g) * p.sq_h + 8 * c;
+    }
+}
+
+// Issue the global loads of a tile into the staging registers.
+template <int D>
+__device__ __forceinline__ void tile_issue(const TreeParams& p, const TileMeta& t, const RowMap<D>& rm,
+                                           Stage<D>& sg) {
+    using Geo = StreamGeom<D>;
+    const int rsub = threadIdx.x / Geo::CPR;
+    const uint16_t* kg = (const uint16_t*)p.k + (t.kvb * p.sk_t + (int64_t)t.kvh * p.sk_h);
+    const uint16_t* vg = (const uint16_t*)p.v + (t.kvb * p.sv_t + (int64_t)t.kvh * p.sv_h);
+    const uint16_t* qg = (const uint16_t*)p.q + ((int64_t)t.start * p.sq_t + (int64_t)t.kvh * p.group * p.sq_h);
+#pragma unroll
+    for (int ps = 0; ps < Geo::PASSES; ++ps) {
+        if (ps * Geo::RPP >= t.rows) break;  // wave-uniform
+        if (ps * Geo::RPP + rsub < t.rows) {
+            sg.k[ps] = ld16(kg + rm.koff[ps]);
+            sg.v[ps] = ld16(vg + rm.voff[ps]);
         }
+    }
+#pragma unroll
+    for (int ps = 0; ps < Geo::PASSES; ++ps) {
+        if (ps * Geo::RPP >= t.nq) break;  // wave-uniform
+        if (ps * Geo::RPP + rsub < t.nq) sg.q[ps] = ld16(qg + rm.qoff[ps]);
     }
 }
 
@@ -568,8 +570,8 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void tree_stream_kernel(
     Stage<D> sg;
     tile_setup<D>(p, plan, sa, cu_lds, w, none, cur);
     if (cur.valid) {
-        tile_rowmap<D>(cur, rm);
-        tile_issue<D>(p, gdiv, cur, rm, sg);
+        tile_rowmap<D>(p, gdiv, cur, rm);
+        tile_issue<D>(p, cur, rm, sg);
     }
     for (;;) {
         // The staged loads must have landed before they are written to LDS;
@@ -586,8 +588,8 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void tree_stream_kernel(
         if (more) {
             const bool fresh = tile_setup<D>(p, plan, sa, cu_lds, wn, cur, nxt);
             if (nxt.valid) {
-                if (fresh) tile_rowmap<D>(nxt, rm);
-                tile_issue<D>(p, gdiv, nxt, rm, sg);
+                if (fresh) tile_rowmap<D>(p, gdiv, nxt, rm);
+                tile_issue<D>(p, nxt, rm, sg);
             }
         }
         if (cur.valid) {
