@@ -34,6 +34,10 @@ def compile_flags() -> list:
         f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
         # packed fp32 VALU ops stay off (correctness issue on this platform)
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+        # one-lane counter atomics stay single instructions: the atomic
+        # optimizer would turn each into a wave reduction that waits for the
+        # answer at once, where the subtree kernel overlaps it with its loads
+        "-Xarch_device", "-mllvm=-amdgpu-atomic-optimizer-strategy=None",
         "-Wall", "-Wno-unused-function",
     ]
 

@@ -98,11 +98,29 @@ struct SubtreePlan {
 };
 
 // Launch arguments of the persistent subtree kernel (subtree_stream.hip).
+// Work items of the subtree kernel: item k of group g is tile index
+// w = k * ngroups + g (w as in the comment of tile_setup).  Workgroup
+// blockIdx = j * ngroups + g starts with item j; with sched set, later items
+// come from the group's counter pair (sched[g * kSchedStride] hands out items
+// gsize, gsize+1, ...; sched[g * kSchedStride + 1] counts the workgroups that
+// are done, and the last one resets both to zero), without it workgroup j
+// takes j, j + gsize, ...  Counter pairs of one launch lie kSchedStride words
+// (1 KB) apart, so no two groups share a cache line: atomics on one line are
+// serialised, and 4000-8000 requests per launch on a single line made the
+// kernel 10-20% slower.  The words in between hold other launches' pairs.
+constexpr int kSchedGroups = 2048;
+constexpr int kSchedSlots = 128;                // launches with counters of their own
+constexpr int kSchedStride = 2 * kSchedSlots;   // words between groups of one launch
+
 struct StreamArgs {
     int32_t n_work;     // tiles over all (sequence, kv head) pairs
     Divider tiles_div;  // tiles per (sequence, kv head)
     Divider hkv_div;    // kv heads
     Divider gdiv;       // q heads per kv head
+    Divider ngroups;    // work groups
+    int32_t gsize;      // workgroups per group (grid = gsize * ngroups)
+    int32_t items;      // items per group (n_work = items * ngroups)
+    uint32_t* sched;    // the launch's counter pairs (zero), or null (static schedule)
 };
 
 // Subtree kernel: rows one tile may stage (K/V rows, Q rows) for head_dim,

@@ -28,6 +28,7 @@
 // with gfx950's transposing LDS load (ds_read_b64_tr_b16), two per MFMA, in
 // the key order in which the S^T output registers form the P^T operand.
 #include <algorithm>
+#include <mutex>
 
 #include "qattn_common.h"
 #include "qattn_device.h"
@@ -61,7 +62,7 @@ struct StreamGeom {
     static constexpr int NC = D / 32;                 // 32-element k-chunks of Q K^T
     static constexpr int ND = D / 16;                 // 16-row d-tiles of O^T
     static constexpr size_t LDS_BYTES = ((size_t)(KV_ROWS + Q_ROWS + V_ROWS) * PITCH) * 2 +
-                                        (size_t)Q_ROWS * sizeof(QueryEntry) + kCuCache * 4;
+                                        (size_t)Q_ROWS * sizeof(QueryEntry) + kCuCache * 4 + 16;
 };
 
 // Per-tile state.  Scalars are wave-uniform; first/cnt/off/qb are per lane,
@@ -536,9 +537,22 @@ __device__ __forceinline__ void tile_compute(const TreeParams& p, const TileMeta
         block_compute<T, D, LSE, PSTATE>(p, t, qb, Ks, Vs, Qs, qt);
 }
 
+// Next item of a group: one returning atomic on the group's counter.
+__device__ __forceinline__ uint32_t sched_grab(uint32_t* ctr) {
+    return __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // The staging registers of one tile stay live across the compute phase of the
 // previous one; 3 workgroups of 256 threads per CU (about 50 KB of LDS each)
 // need at most 168 VGPRs.
+//
+// Schedule (StreamArgs): workgroup j of group g takes item j first.  With
+// counters, thread 0 asks for the next item while the loads of the current
+// one are in flight, and the answer is waited for with those loads, so the
+// counter's latency is hidden; workgroups that started late or ran slow take
+// fewer items.  Every workgroup that took part adds one to the group's done
+// counter after its last request, and the last of them clears both counters,
+// so the next launch finds them at zero.
 template <typename T, int D, bool LSE, bool PSTATE>
 __global__ __launch_bounds__(kStThreads)
 __attribute__((amdgpu_waves_per_eu(3, 3))) void tree_stream_kernel(
@@ -550,10 +564,21 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void tree_stream_kernel(
     uint16_t* Vs = Qs + Geo::Q_ROWS * Geo::PITCH;
     QueryEntry* qtab = reinterpret_cast<QueryEntry*>(Vs + Geo::V_ROWS * Geo::PITCH);
     int32_t* cuc = reinterpret_cast<int32_t*>(qtab + Geo::Q_ROWS);
+    int32_t* next_slot = cuc + kCuCache;  // the workgroup's next item, written by thread 0
     const Divider gdiv = sa.gdiv;
 
-    int w = blockIdx.x;
-    if (w >= sa.n_work) return;  // uniform: no barrier below is skipped by a subset of waves
+    const int grp = divide((int)blockIdx.x, sa.ngroups);
+    const int g = (int)blockIdx.x - grp * sa.ngroups.d;  // group
+    int k = grp;                                         // current item
+    if (k >= sa.items) return;  // uniform: no barrier below is skipped by a subset of waves
+    const bool dyn = sa.sched != nullptr;
+    uint32_t* grab_ctr = dyn ? sa.sched + (size_t)g * kSchedStride : nullptr;
+    uint32_t* done_ctr = dyn ? grab_ctr + 1 : nullptr;
+    const bool leader = threadIdx.x == 0;
+    // ans: the answer of this workgroup's last counter request (one variable,
+    // so it stays in one register while the request is in flight)
+    uint32_t ans = 0;
+    const int w = k * sa.ngroups.d + g;
     for (int i = threadIdx.x; i <= p.B; i += kStThreads) cuc[i] = p.cu[i];  // p.B < kCuCache
     // V rows the PV product reads but no tile has written yet must hold finite
     // values (P = 0 multiplies them): zero them once
@@ -573,6 +598,7 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void tree_stream_kernel(
         tile_rowmap<D>(p, gdiv, cur, rm);
         tile_issue<D>(p, cur, rm, sg);
     }
+    if (dyn && leader) ans = sched_grab(grab_ctr);  // answered by the first loop top
     for (;;) {
         // The staged loads must have landed before they are written to LDS;
         // waiting for all vector memory here (the previous tile's O stores
@@ -581,9 +607,11 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void tree_stream_kernel(
         // a conservative wait on every outstanding store.
         __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
         if (cur.valid) tile_store<D>(cur, Ks, Vs, Qs, sg);
+        if (leader) *next_slot = dyn ? sa.gsize + (int)ans : k + sa.gsize;
         __syncthreads();
-        const int wn = w + gridDim.x;
-        const bool more = wn < sa.n_work;
+        const int kn = __builtin_amdgcn_readfirstlane(*next_slot);
+        const bool more = kn < sa.items;
+        const int wn = kn * sa.ngroups.d + g;
         TileMeta nxt;
         if (more) {
             const bool fresh = tile_setup<D>(p, plan, sa, cu_lds, wn, cur, nxt);
@@ -592,6 +620,8 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void tree_stream_kernel(
                 tile_issue<D>(p, nxt, rm, sg);
             }
         }
+        // the next item, or (after this workgroup's last request) done
+        if (dyn && leader) ans = sched_grab(more ? grab_ctr : done_ctr);
         if (cur.valid) {
             // the query table follows the tile shape (uniform branch)
             if (cur.tile != tab_tile || cur.n != tab_n) {
@@ -605,8 +635,58 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void tree_stream_kernel(
         __syncthreads();
         if (!more) break;
         cur = nxt;
-        w = wn;
+        k = kn;
     }
+    // The last workgroup of the group to finish clears its counters: every
+    // other one has made its last request before adding to done_ctr.
+    const int members = sa.items < sa.gsize ? sa.items : sa.gsize;
+    if (dyn && leader && ans == (uint32_t)(members - 1)) {
+        __hip_atomic_store(grab_ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(done_ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+// Scheduler counters (StreamArgs::sched): per device one allocation of
+// kSchedGroups * kSchedStride words, zeroed once, holding kSchedSlots counter
+// slots (a slot: one counter pair per group, kSchedStride words apart).  Every
+// launch leaves its slot at zero when it completes.  Eager launches take the
+// first kSchedRing slots in turn, so launches that overlap in time use
+// different slots unless more than kSchedRing of them are in flight at once.
+// A launch recorded into a graph keeps one of the other slots for every
+// replay (replays of one graph run in stream order); when those run out, or
+// when the first launch on a device is being recorded (no allocation then),
+// the kernel uses the static schedule.
+constexpr int kSchedRing = 32, kSchedMaxDev = 64;
+
+static uint32_t* sched_counters(int dev, hipStream_t st) {
+    static std::mutex mu;
+    static uint32_t* pool[kSchedMaxDev] = {};
+    static int ring_next[kSchedMaxDev] = {}, captured_next[kSchedMaxDev] = {};
+    if (dev < 0 || dev >= kSchedMaxDev) return nullptr;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &cs) != hipSuccess) return nullptr;
+    const bool capturing = cs != hipStreamCaptureStatusNone;
+    std::lock_guard<std::mutex> lock(mu);
+    if (!pool[dev]) {
+        if (capturing) return nullptr;
+        const size_t bytes = (size_t)kSchedGroups * kSchedStride * sizeof(uint32_t);
+        void* ptr = nullptr;
+        if (hipMalloc(&ptr, bytes) != hipSuccess) return nullptr;
+        if (hipMemset(ptr, 0, bytes) != hipSuccess) {
+            (void)hipFree(ptr);
+            return nullptr;
+        }
+        pool[dev] = (uint32_t*)ptr;
+    }
+    int slot;
+    if (capturing) {
+        if (captured_next[dev] >= kSchedSlots - kSchedRing) return nullptr;
+        slot = kSchedRing + captured_next[dev]++;
+    } else {
+        slot = ring_next[dev];
+        ring_next[dev] = (slot + 1) % kSchedRing;
+    }
+    return pool[dev] + 2 * slot;
 }
 
 template <typename T, int D, bool LSE, bool PSTATE>
@@ -632,15 +712,24 @@ static int launch_stream_t(const TreeParams& p, const SubtreePlan& plan, hipStre
         return QATTN_ERR_HIP;
     }
     // a multiple of the tile count when possible: each workgroup then keeps one
-    // tile index and reuses its level table across (sequence, kv head) pairs
+    // tile index (its group) and reuses its level table across (sequence, kv
+    // head) pairs; otherwise one group over all tiles
     const int64_t cap = (int64_t)std::max(cus, 1) * std::max(per_cu, 1);
     int64_t grid = std::min<int64_t>(n_work, cap);
-    if (plan.total_tiles <= cap && grid < n_work) grid = cap / plan.total_tiles * plan.total_tiles;
+    int64_t ngroups = 1;
+    if (plan.total_tiles <= cap) {
+        ngroups = plan.total_tiles;
+        grid = std::max<int64_t>(1, std::min<int64_t>(n_work, cap) / ngroups) * ngroups;
+    }
     StreamArgs sa;
     sa.n_work = (int32_t)n_work;
     sa.tiles_div = make_divider(plan.total_tiles);
     sa.hkv_div = make_divider(p.Hkv);
     sa.gdiv = make_divider(p.group);
+    sa.ngroups = make_divider((int32_t)ngroups);
+    sa.gsize = (int32_t)(grid / ngroups);
+    sa.items = (int32_t)(n_work / ngroups);
+    sa.sched = (ngroups <= kSchedGroups && sa.items > sa.gsize) ? sched_counters(dev, st) : nullptr;
     hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(kStThreads), lds, st, p, plan, sa);
     return launch_status("tree_stream_kernel");
 }

@@ -404,28 +404,57 @@ def test_baseline_full_size(B, b, d):
     say("full size", B, b, d)
     Q, K, V, cu = tree_case(B, b, d, 32, 128)
     o_ref, lse_ref, _ = oracle_tree(Q, K, V, cu, b, d)
-    for algo in (0, 1):
+    for algo in (0, 1, 2):
         o, l = run_tree(Q, K, V, cu, b, d, algo=algo)
         check_fp16(o, o_ref, f"full algo {algo}")
         assert np.abs(l - lse_ref).max() <= 1e-4
 
 
-def test_graph_capture_replay():
-    """The entry point records into a HIP graph (device cu + max_seqlen) and
-    every replay matches the eager result, with eager work in between."""
+def test_subtree_schedule_repeats():
+    """The subtree kernel hands out tiles from counters that each launch
+    leaves at zero when it completes, taken from a ring of 32 per device:
+    140 launches at a size that uses them (mixed with small launches that do
+    not) reuse every slot, and every result is bit-identical to the first."""
     ra, _ = _ra()
-    Q, K, V, cu = tree_case(4, 4, 4, 8, 128)
+    B, b, d = 4, 4, 5
+    Q, K, V, cu = tree_case(B, b, d, 32, 128)
+    o_ref, _, _ = oracle_tree(Q, K, V, cu, b, d)
     Qd, Kd, Vd, cud = Q.to(DEV), K.to(DEV), V.to(DEV), cu.to(DEV)
-    N = num_tree_nodes(4, 4)
-    eager = ra.ragged_attention(Qd, Kd, Vd, cud, 4, 4, max_seqlen=N)
+    N = num_tree_nodes(b, d)
+    first, _ = ra._tree_forward(Qd, Kd, Vd, cud, b, d, N, False, 2)
+    check_fp16(first.float().cpu().double().numpy(), o_ref, "first launch")
+    q2, k2, v2, cu2 = tree_case(2, 2, 3, 4, 64)
+    small_ref, _ = ra._tree_forward(q2.to(DEV), k2.to(DEV), v2.to(DEV), cu2.to(DEV), 2, 3, None, False, 2)
+    for i in range(140):
+        if i % 9 == 4:
+            small, _ = ra._tree_forward(q2.to(DEV), k2.to(DEV), v2.to(DEV), cu2.to(DEV), 2, 3, None, False, 2)
+            assert torch.equal(small, small_ref), f"small launch {i}"
+        o, _ = ra._tree_forward(Qd, Kd, Vd, cud, b, d, N, False, 2)
+        if i % 10 == 9 or i > 125:
+            assert torch.equal(o, first), f"launch {i}"
+    torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("B,b,d,H", [(4, 4, 4, 8), (4, 4, 5, 32)])
+def test_graph_capture_replay(B, b, d, H):
+    """The entry point records into a HIP graph (device cu + max_seqlen) and
+    every replay matches the eager result, with eager work in between (the
+    full-size case records the subtree kernel with its counter slot, which
+    every replay reuses)."""
+    say("graph", B, b, d, H)
+    ra, _ = _ra()
+    Q, K, V, cu = tree_case(B, b, d, H, 128)
+    Qd, Kd, Vd, cud = Q.to(DEV), K.to(DEV), V.to(DEV), cu.to(DEV)
+    N = num_tree_nodes(b, d)
+    eager = ra.ragged_attention(Qd, Kd, Vd, cud, b, d, max_seqlen=N)
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
-        ra.ragged_attention(Qd, Kd, Vd, cud, 4, 4, max_seqlen=N)
+        ra.ragged_attention(Qd, Kd, Vd, cud, b, d, max_seqlen=N)
     torch.cuda.current_stream().wait_stream(s)
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
-        out = ra.ragged_attention(Qd, Kd, Vd, cud, 4, 4, max_seqlen=N)
+        out = ra.ragged_attention(Qd, Kd, Vd, cud, b, d, max_seqlen=N)
     for i in range(4):
         out.zero_()
         junk = torch.randn(1000, device=DEV).sum()  # eager work between replays
