@@ -74,13 +74,16 @@ struct TileMeta {
     int32_t first, cnt, off, qb;
 };
 
-// Element offsets of this thread's loads of a tile, relative to the tile's
-// K, V and Q base addresses: K/V pass ps reads LDS row ps * RPP + tid / CPR,
-// Q pass ps Q row ps * RPP + tid / CPR (chunk tid % CPR).  They depend only on
-// the level table, so a workgroup that stays on one tile computes them once.
+// Rows of this thread's loads of a tile (chunk tid % CPR of each): K/V pass ps
+// stages LDS row ps * RPP + tid / CPR, which is K/V row kvrow[ps] past the
+// tile's kv base; Q pass ps stages Q row ps * RPP + tid / CPR, which is token
+// qrow[ps] >> 8 past the tile's start at q head qrow[ps] & 255 past the kv
+// head's first.  They depend only on the level table, so a workgroup that
+// stays on one tile computes them once; 32-bit rows keep them in few
+// registers (the 64-bit element offsets are formed at issue).
 template <int D>
 struct RowMap {
-    int64_t koff[StreamGeom<D>::PASSES], voff[StreamGeom<D>::PASSES], qoff[StreamGeom<D>::PASSES];
+    int32_t kvrow[StreamGeom<D>::PASSES], qrow[StreamGeom<D>::PASSES];
 };
 
 template <int D>
@@ -97,14 +100,20 @@ void stream_tile_caps(int head_dim, int* kv_rows, int* q_rows) {
     *q_rows = rows;
 }
 
+// Sequence of tile index w = (seq * Hkv + kvh) * tiles + tile.
+__device__ __forceinline__ int tile_seq(const StreamArgs& sa, int w) {
+    return divide(divide(w, sa.tiles_div), sa.hkv_div);
+}
+
 // Which tile w is, and its level table (src/ragged_attn.py:376-377 walk:
 // the ancestors of roots r0..r1-1 at level lo are, per level, one contiguous
-// node range).  Returns true when the level table was (re)computed, false
-// when it was taken from prev (same tile index and sequence length).
+// node range), for a sequence spanning tokens [s, e) (cu_seqlens[seq],
+// cu_seqlens[seq + 1], wave-uniform).  Returns true when the level table was
+// (re)computed, false when it was taken from prev (same tile index and
+// sequence length).
 template <int D>
-__device__ __forceinline__ bool tile_setup(const TreeParams& p, const SubtreePlan& plan, const StreamArgs& sa,
-                                           const int32_t __attribute__((address_space(3)))* cu_lds, int w,
-                                           const TileMeta& prev, TileMeta& t) {
+__device__ __forceinline__ bool tile_setup_se(const TreeParams& p, const SubtreePlan& plan, const StreamArgs& sa,
+                                              int w, int32_t s, int32_t e, const TileMeta& prev, TileMeta& t) {
     const int lane = threadIdx.x & 63;
     t.valid = 0;
     t.rows = t.nq = 0;
@@ -124,13 +133,6 @@ __device__ __forceinline__ bool tile_setup(const TreeParams& p, const SubtreePla
     t.seq = seq;
     t.kvh = pair - seq * p.Hkv;
     if (seq >= p.B) return true;
-    // cu_seqlens from the workgroup's LDS copy (the host launches this kernel
-    // only for B < kCuCache): a global load here would make the wait for it
-    // also wait for every O store still in flight.  readfirstlane: the offsets
-    // are wave-uniform, so every tile scalar derived from them stays in SGPRs
-    // and every branch on them is a scalar branch.
-    const int32_t s = __builtin_amdgcn_readfirstlane(cu_lds[seq]);
-    const int32_t e = __builtin_amdgcn_readfirstlane(cu_lds[seq + 1]);
     if (s < 0 || e < s || (int64_t)e > p.total_tokens) return true;
     int32_t n = e - s;
     if (n > p.max_seqlen) n = p.max_seqlen;
@@ -229,6 +231,22 @@ __device__ __forceinline__ bool tile_setup(const TreeParams& p, const SubtreePla
     return true;
 }
 
+// tile_setup_se with the sequence bounds from the workgroup's LDS copy of
+// cu_seqlens (the host launches this kernel only for B < kCuCache): a global
+// load here would make the wait for it also wait for every O store still in
+// flight.  readfirstlane: the offsets are wave-uniform, so every tile scalar
+// derived from them stays in SGPRs and every branch on them is a scalar branch.
+template <int D>
+__device__ __forceinline__ bool tile_setup(const TreeParams& p, const SubtreePlan& plan, const StreamArgs& sa,
+                                           const int32_t __attribute__((address_space(3)))* cu_lds, int w,
+                                           const TileMeta& prev, TileMeta& t) {
+    int seq = tile_seq(sa, w);
+    seq = seq < p.B ? seq : p.B;  // tile_setup_se rejects seq >= B
+    const int32_t s = __builtin_amdgcn_readfirstlane(cu_lds[seq]);
+    const int32_t e = __builtin_amdgcn_readfirstlane(cu_lds[seq < p.B ? seq + 1 : seq]);
+    return tile_setup_se<D>(p, plan, sa, w, s, e, prev, t);
+}
+
 template <int D>
 __device__ __forceinline__ void tile_rowmap(const TreeParams& p, const Divider& gdiv, const TileMeta& t,
                                             RowMap<D>& rm) {
@@ -263,14 +281,13 @@ __device__ __forceinline__ void tile_rowmap(const TreeParams& p, const Divider& 
         }
     }
     const int g = p.group;
+    (void)c;
 #pragma unroll
     for (int ps = 0; ps < Geo::PASSES; ++ps) {
-        const int64_t node = ps * Geo::RPP + rsub - kof[ps];  // K/V row relative to the tile's kv base
-        rm.koff[ps] = node * p.sk_t + 8 * c;
-        rm.voff[ps] = node * p.sv_t + 8 * c;
+        rm.kvrow[ps] = ps * Geo::RPP + rsub - kof[ps];  // K/V row relative to the tile's kv base
         const int sq = ps * Geo::RPP + rsub - qbl[ps];
         const int nd = divide(sq, gdiv);
-        rm.qoff[ps] = (int64_t)(fl[ps] + nd) * p.sq_t + (int64_t)(sq - nd * g) * p.sq_h + 8 * c;
+        rm.qrow[ps] = ((fl[ps] + nd) << 8) | (sq - nd * g);  // group <= Q_ROWS (a plan exists)
     }
 }
 
@@ -280,21 +297,24 @@ __device__ __forceinline__ void tile_issue(const TreeParams& p, const TileMeta& 
                                            Stage<D>& sg) {
     using Geo = StreamGeom<D>;
     const int rsub = threadIdx.x / Geo::CPR;
-    const uint16_t* kg = (const uint16_t*)p.k + (t.kvb * p.sk_t + (int64_t)t.kvh * p.sk_h);
-    const uint16_t* vg = (const uint16_t*)p.v + (t.kvb * p.sv_t + (int64_t)t.kvh * p.sv_h);
-    const uint16_t* qg = (const uint16_t*)p.q + ((int64_t)t.start * p.sq_t + (int64_t)t.kvh * p.group * p.sq_h);
+    const int c8 = 8 * (threadIdx.x % Geo::CPR);
+    const uint16_t* kg = (const uint16_t*)p.k + (t.kvb * p.sk_t + (int64_t)t.kvh * p.sk_h + c8);
+    const uint16_t* vg = (const uint16_t*)p.v + (t.kvb * p.sv_t + (int64_t)t.kvh * p.sv_h + c8);
+    const uint16_t* qg =
+        (const uint16_t*)p.q + ((int64_t)t.start * p.sq_t + (int64_t)t.kvh * p.group * p.sq_h + c8);
 #pragma unroll
     for (int ps = 0; ps < Geo::PASSES; ++ps) {
         if (ps * Geo::RPP >= t.rows) break;  // wave-uniform
         if (ps * Geo::RPP + rsub < t.rows) {
-            sg.k[ps] = ld16(kg + rm.koff[ps]);
-            sg.v[ps] = ld16(vg + rm.voff[ps]);
+            sg.k[ps] = ld16(kg + (int64_t)rm.kvrow[ps] * p.sk_t);
+            sg.v[ps] = ld16(vg + (int64_t)rm.kvrow[ps] * p.sv_t);
         }
     }
 #pragma unroll
     for (int ps = 0; ps < Geo::PASSES; ++ps) {
         if (ps * Geo::RPP >= t.nq) break;  // wave-uniform
-        if (ps * Geo::RPP + rsub < t.nq) sg.q[ps] = ld16(qg + rm.qoff[ps]);
+        if (ps * Geo::RPP + rsub < t.nq)
+            sg.q[ps] = ld16(qg + (int64_t)(rm.qrow[ps] >> 8) * p.sq_t + (int64_t)(rm.qrow[ps] & 255) * p.sq_h);
     }
 }
 
@@ -393,23 +413,32 @@ __device__ __forceinline__ void block_compute(const TreeParams& p, const TileMet
     const int qh = t.kvh * g + qe.hoff;
 
     // ---- S^T = K Q^T ----
+    // Every key tile of the LDS buffer is multiplied (rows past the tile hold
+    // stale but finite data or whatever LDS held; the row mask below selects
+    // -inf for them).  Software-pipelined: the K operand of step i + 1 is read
+    // before the product of step i is issued, and consecutive products
+    // accumulate into different key tiles.
     Vec16 qf[NC];
 #pragma unroll
     for (int kc = 0; kc < NC; ++kc) qf[kc] = ld16(Qs + (16 * qb + c16) * Geo::PITCH + 32 * kc + 8 * i4);
-    const int kt_used = (t.rows + 15) / 16;
     f4_t sacc[KT];
 #pragma unroll
-    for (int kt = 0; kt < KT; ++kt) {
-        sacc[kt] = f4_t{0.f, 0.f, 0.f, 0.f};
-        if (kt < kt_used) {  // wave-uniform
+    for (int kt = 0; kt < KT; ++kt) sacc[kt] = f4_t{0.f, 0.f, 0.f, 0.f};
+    {
+        constexpr int NS = KT * NC;  // step i: kc = i / KT, kt = i % KT
+        Vec16 kb[2];
+        kb[0] = ld16(Ks + c16 * Geo::PITCH + 8 * i4);
 #pragma unroll
-            for (int kc = 0; kc < NC; ++kc) {
-                const Vec16 a = ld16(Ks + (16 * kt + c16) * Geo::PITCH + 32 * kc + 8 * i4);
-                sacc[kt] = MfmaOps<T>::mma(a, qf[kc], sacc[kt]);
+        for (int i = 0; i < NS; ++i) {
+            if (i + 1 < NS) {
+                const int kc1 = (i + 1) / KT, kt1 = (i + 1) % KT;
+                kb[(i + 1) & 1] = ld16(Ks + (16 * kt1 + c16) * Geo::PITCH + 32 * kc1 + 8 * i4);
             }
+            sacc[i % KT] = MfmaOps<T>::mma(kb[i & 1], qf[i / KT], sacc[i % KT]);
         }
     }
 
+    __builtin_amdgcn_sched_barrier(0);  // keep the PV operand reads below the softmax
     // ---- masked softmax per query column ----
     float mx = -INFINITY;
 #pragma unroll
@@ -491,19 +520,27 @@ __device__ __forceinline__ void block_compute(const TreeParams& p, const TileMet
             plo[kk].w[2 * h + 1] = MfmaOps<T>::pack2(pv[2] - MfmaOps<T>::lo(h23), pv[3] - MfmaOps<T>::hi(h23));
         }
     }
-    const int kk_used = (t.rows + 31) / 32;
+    __builtin_amdgcn_sched_barrier(0);
+    // All V_ROWS rows take part (P = 0 past the tile; those rows hold finite
+    // values).  Software-pipelined like S: step i = (kk, dt), kk = i / ND,
+    // reads its V^T operand one step ahead.
+    {
+        constexpr int NS = 2 * ND;
+        uint2 va[2], vb[2];
+        // A[d][e]: e = 0..3 -> key 32 kk + 4 i4 + e, e = 4..7 -> key 32 kk + 16 + 4 i4 + (e - 4)
+        va[0] = vt_read4(Vs, Geo::PITCH, 4 * i4, 0, c16);
+        vb[0] = vt_read4(Vs, Geo::PITCH, 16 + 4 * i4, 0, c16);
 #pragma unroll
-    for (int dt = 0; dt < ND; ++dt) {
-#pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
-            if (kk < kk_used) {  // wave-uniform
-                // A[d][e]: e = 0..3 -> key 32 kk + 4 i4 + e, e = 4..7 -> key 32 kk + 16 + 4 i4 + (e - 4)
-                const uint2 a0 = vt_read4(Vs, Geo::PITCH, 32 * kk + 4 * i4, 16 * dt, c16);
-                const uint2 a1 = vt_read4(Vs, Geo::PITCH, 32 * kk + 16 + 4 * i4, 16 * dt, c16);
-                const Vec16 a = Vec16{{a0.x, a0.y, a1.x, a1.y}};
-                oacc[dt] = MfmaOps<T>::mma(a, phi[kk], oacc[dt]);
-                oacc[dt] = MfmaOps<T>::mma(a, plo[kk], oacc[dt]);
+        for (int i = 0; i < NS; ++i) {
+            if (i + 1 < NS) {
+                const int kk1 = (i + 1) / ND, dt1 = (i + 1) % ND;
+                va[(i + 1) & 1] = vt_read4(Vs, Geo::PITCH, 32 * kk1 + 4 * i4, 16 * dt1, c16);
+                vb[(i + 1) & 1] = vt_read4(Vs, Geo::PITCH, 32 * kk1 + 16 + 4 * i4, 16 * dt1, c16);
             }
+            const int kk = i / ND, dt = i % ND;
+            const Vec16 a = Vec16{{va[i & 1].x, va[i & 1].y, vb[i & 1].x, vb[i & 1].y}};
+            oacc[dt] = MfmaOps<T>::mma(a, phi[kk], oacc[dt]);
+            oacc[dt] = MfmaOps<T>::mma(a, plo[kk], oacc[dt]);
         }
     }
 
@@ -579,26 +616,32 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void tree_stream_kernel(
     // so it stays in one register while the request is in flight)
     uint32_t ans = 0;
     const int w = k * sa.ngroups.d + g;
-    for (int i = threadIdx.x; i <= p.B; i += kStThreads) cuc[i] = p.cu[i];  // p.B < kCuCache
     // V rows the PV product reads but no tile has written yet must hold finite
     // values (P = 0 multiplies them): zero them once
     for (int i = threadIdx.x; i < Geo::V_ROWS * Geo::PITCH / 8; i += kStThreads)
         st16(Vs + 8 * i, Vec16{{0u, 0u, 0u, 0u}});
-    __syncthreads();
     const int32_t __attribute__((address_space(3)))* cu_lds =
         (const int32_t __attribute__((address_space(3)))*)cuc;
 
+    // The first tile takes the bounds of its sequence from wave-uniform
+    // loads, and the LDS copy of cu_seqlens is written at the first loop top,
+    // so nothing here waits for vector memory.
     TileMeta cur, none;
     none.valid = 0;
     int tab_tile = -1, tab_n = -1;  // shape the query table was built for
     RowMap<D> rm;
     Stage<D> sg;
-    tile_setup<D>(p, plan, sa, cu_lds, w, none, cur);
+    const int seq0 = tile_seq(sa, w);  // < p.B: w < n_work
+    const int32_t cu_mine = threadIdx.x <= p.B ? p.cu[threadIdx.x] : 0;  // p.B < kCuCache = kStThreads
+    const int32_t s0 = __builtin_amdgcn_readfirstlane(p.cu[seq0]);
+    const int32_t e0 = __builtin_amdgcn_readfirstlane(p.cu[seq0 + 1]);
+    tile_setup_se<D>(p, plan, sa, w, s0, e0, none, cur);
     if (cur.valid) {
         tile_rowmap<D>(p, gdiv, cur, rm);
         tile_issue<D>(p, cur, rm, sg);
     }
     if (dyn && leader) ans = sched_grab(grab_ctr);  // answered by the first loop top
+    bool first = true;
     for (;;) {
         // The staged loads must have landed before they are written to LDS;
         // waiting for all vector memory here (the previous tile's O stores
@@ -606,6 +649,8 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void tree_stream_kernel(
         // a load pending into the issue code below, which would otherwise get
         // a conservative wait on every outstanding store.
         __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+        if (first && threadIdx.x <= p.B) cuc[threadIdx.x] = cu_mine;
+        first = false;
         if (cur.valid) tile_store<D>(cur, Ks, Vs, Qs, sg);
         if (leader) *next_slot = dyn ? sa.gsize + (int)ans : k + sa.gsize;
         __syncthreads();

@@ -281,6 +281,30 @@ def test_ragged_and_truncated(lens, b, md):
         assert np.abs(l - lse_ref).max() <= 1e-4
 
 
+@pytest.mark.parametrize("cu_list,max_seqlen,b,d,H", [
+    ([5, 20, 30], 15, 2, 3, 4),
+    ([0, 15, 25, 40], 15, 2, 3, 4),
+    ([65, 1430, 2730, 4095, 5460], 1365, 4, 5, 8),
+])
+def test_shifted_cu_seqlens(cu_list, max_seqlen, b, d, H):
+    """cu_seqlens that do not start at 0 or leave a sequence short of
+    max_seqlen, with batch * max_seqlen rows (the subtree kernel reads each
+    workgroup's first sequence bounds apart from its LDS copy of
+    cu_seqlens); the last case is large enough for the counter schedule.
+    Rows outside [cu[0], cu[B]) belong to no sequence and are not compared."""
+    say("shifted cu", cu_list, max_seqlen, b, d, H)
+    B = len(cu_list) - 1
+    T = B * max_seqlen
+    gen = torch.Generator().manual_seed(4242 + T)
+    Q, K, V = [torch.randn(T, H, 128, generator=gen).half() for _ in range(3)]
+    cu = torch.tensor(cu_list, dtype=torch.int32)
+    o_ref, lse_ref, _ = oracle_tree(Q, K, V, cu, b, d)
+    o, l = run_tree(Q, K, V, cu, b, d, algo=2, max_seqlen=max_seqlen)
+    rows = slice(cu_list[0], cu_list[-1])
+    check_fp16(o[rows], o_ref[rows], "shifted cu")
+    assert np.abs(l[rows] - lse_ref[rows]).max() <= 1e-4
+
+
 def test_max_seqlen_given_and_device_cu():
     """Graph-friendly call: device cu_seqlens + explicit max_seqlen (no host sync)."""
     Q, K, V, cu = make_inputs([13, 40, 7], 4, 64, 99)
