@@ -150,6 +150,12 @@ struct MfmaOps<F16> {
         return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8_t, a), __builtin_bit_cast(h8_t, b), c, 0,
                                                      0, 0);
     }
+    // 16x16x16: lane (c, i) feeds A[c][4i..4i+3] and B[4i..4i+3][c]
+    static __device__ __forceinline__ f4_t mma16(uint2 a, uint2 b, f4_t c) {
+        typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
+        return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(h4_t, a), __builtin_bit_cast(h4_t, b), c, 0, 0,
+                                                    0);
+    }
     static __device__ __forceinline__ uint32_t pack2(float x, float y) {
         h2_t h;
         h[0] = (_Float16)x;
@@ -166,6 +172,11 @@ struct MfmaOps<BF16> {
     static __device__ __forceinline__ f4_t mma(const Vec16& a, const Vec16& b, f4_t c) {
         return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(b8_t, a), __builtin_bit_cast(b8_t, b), c, 0,
                                                       0, 0);
+    }
+    static __device__ __forceinline__ f4_t mma16(uint2 a, uint2 b, f4_t c) {
+        typedef short s4_t __attribute__((ext_vector_type(4)));
+        return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s4_t, a), __builtin_bit_cast(s4_t, b), c, 0,
+                                                        0, 0);
     }
     static __device__ __forceinline__ uint32_t pack2(float x, float y) {
         b2_t h;

@@ -57,7 +57,7 @@ struct StreamGeom {
     static constexpr int KV_ROWS = PASSES * RPP;      // K/V rows per tile (48 or 64)
     static constexpr int Q_ROWS = KV_ROWS;            // queries per tile
     static constexpr int PITCH = D + 16;              // K, V and Q row pitch (elements)
-    static constexpr int V_ROWS = 64;                 // V rows the PV product reads (2 x 32 keys)
+    static constexpr int V_ROWS = KV_ROWS;            // V rows the PV product reads
     static constexpr int KT = KV_ROWS / 16;           // 16-key tiles of S^T
     static constexpr int NC = D / 32;                 // 32-element k-chunks of Q K^T
     static constexpr int ND = D / 16;                 // 16-row d-tiles of O^T
@@ -501,46 +501,50 @@ __device__ __forceinline__ void block_compute(const TreeParams& p, const TileMet
     ls = col4_sum(ls);
 
     // ---- O^T = V^T P^T, P = hi + lo in T ----
-    Vec16 phi[2], plo[2];
+    // Key tiles 2kk and 2kk+1 form the 32-key operands of 16x16x32 products;
+    // an odd last key tile (48-row tiles) is a 16x16x16 product.
+    constexpr int KF = KT / 2;        // 32-key chunks
+    constexpr bool KTAIL = KT & 1;    // one 16-key chunk
+    uint32_t ph[KT][2], pl[KT][2];    // P hi / lo of key tile kt, packed pairs
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
+    for (int kt = 0; kt < KT; ++kt) {
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-            const int kt = 2 * kk + h;
-            float pv[4] = {0.f, 0.f, 0.f, 0.f};
-            if (kt < KT) {
-#pragma unroll
-                for (int r = 0; r < 4; ++r) pv[r] = sacc[kt][r];
-            }
-            const uint32_t h01 = MfmaOps<T>::pack2(pv[0], pv[1]);
-            const uint32_t h23 = MfmaOps<T>::pack2(pv[2], pv[3]);
-            phi[kk].w[2 * h] = h01;
-            phi[kk].w[2 * h + 1] = h23;
-            plo[kk].w[2 * h] = MfmaOps<T>::pack2(pv[0] - MfmaOps<T>::lo(h01), pv[1] - MfmaOps<T>::hi(h01));
-            plo[kk].w[2 * h + 1] = MfmaOps<T>::pack2(pv[2] - MfmaOps<T>::lo(h23), pv[3] - MfmaOps<T>::hi(h23));
+            const float x = sacc[kt][2 * h], y = sacc[kt][2 * h + 1];
+            const uint32_t w = MfmaOps<T>::pack2(x, y);
+            ph[kt][h] = w;
+            pl[kt][h] = MfmaOps<T>::pack2(x - MfmaOps<T>::lo(w), y - MfmaOps<T>::hi(w));
         }
     }
     __builtin_amdgcn_sched_barrier(0);
     // All V_ROWS rows take part (P = 0 past the tile; those rows hold finite
-    // values).  Software-pipelined like S: step i = (kk, dt), kk = i / ND,
+    // values).  Software-pipelined like S: step i = (chunk, dt), chunk = i / ND,
     // reads its V^T operand one step ahead.
     {
-        constexpr int NS = 2 * ND;
+        constexpr int NS = (KF + (KTAIL ? 1 : 0)) * ND;
+        // A[d][e] of chunk kk: e = 0..3 -> key 32 kk + 4 i4 + e, e = 4..7 -> key
+        // 32 kk + 16 + 4 i4 + (e - 4); the 16-key tail: e = 0..3 -> key 32 KF + 4 i4 + e
         uint2 va[2], vb[2];
-        // A[d][e]: e = 0..3 -> key 32 kk + 4 i4 + e, e = 4..7 -> key 32 kk + 16 + 4 i4 + (e - 4)
-        va[0] = vt_read4(Vs, Geo::PITCH, 4 * i4, 0, c16);
-        vb[0] = vt_read4(Vs, Geo::PITCH, 16 + 4 * i4, 0, c16);
+        auto fetch = [&](int i, uint2& x, uint2& y) {
+            const int kk = i / ND, dt = i % ND;
+            x = vt_read4(Vs, Geo::PITCH, 32 * kk + 4 * i4, 16 * dt, c16);
+            if (kk < KF) y = vt_read4(Vs, Geo::PITCH, 32 * kk + 16 + 4 * i4, 16 * dt, c16);
+        };
+        fetch(0, va[0], vb[0]);
 #pragma unroll
         for (int i = 0; i < NS; ++i) {
-            if (i + 1 < NS) {
-                const int kk1 = (i + 1) / ND, dt1 = (i + 1) % ND;
-                va[(i + 1) & 1] = vt_read4(Vs, Geo::PITCH, 32 * kk1 + 4 * i4, 16 * dt1, c16);
-                vb[(i + 1) & 1] = vt_read4(Vs, Geo::PITCH, 32 * kk1 + 16 + 4 * i4, 16 * dt1, c16);
-            }
+            if (i + 1 < NS) fetch(i + 1, va[(i + 1) & 1], vb[(i + 1) & 1]);
             const int kk = i / ND, dt = i % ND;
-            const Vec16 a = Vec16{{va[i & 1].x, va[i & 1].y, vb[i & 1].x, vb[i & 1].y}};
-            oacc[dt] = MfmaOps<T>::mma(a, phi[kk], oacc[dt]);
-            oacc[dt] = MfmaOps<T>::mma(a, plo[kk], oacc[dt]);
+            if (kk < KF) {
+                const Vec16 a = Vec16{{va[i & 1].x, va[i & 1].y, vb[i & 1].x, vb[i & 1].y}};
+                const Vec16 bh = Vec16{{ph[2 * kk][0], ph[2 * kk][1], ph[2 * kk + 1][0], ph[2 * kk + 1][1]}};
+                const Vec16 bl = Vec16{{pl[2 * kk][0], pl[2 * kk][1], pl[2 * kk + 1][0], pl[2 * kk + 1][1]}};
+                oacc[dt] = MfmaOps<T>::mma(a, bh, oacc[dt]);
+                oacc[dt] = MfmaOps<T>::mma(a, bl, oacc[dt]);
+            } else {
+                oacc[dt] = MfmaOps<T>::mma16(va[i & 1], make_uint2(ph[KT - 1][0], ph[KT - 1][1]), oacc[dt]);
+                oacc[dt] = MfmaOps<T>::mma16(va[i & 1], make_uint2(pl[KT - 1][0], pl[KT - 1][1]), oacc[dt]);
+            }
         }
     }
 
