@@ -11,8 +11,11 @@ independent sets whose total exceeds 512 MB, so MI355X's 256 MB Infinity
 Cache cannot serve a call from the previous call's data.  The calls are
 captured in HIP graphs (the reference times CUDA-graph replays,
 scripts/benchmark_micro.py:169-187), 8 calls per graph so graph-launch gaps do
-not pad the per-call time; the timed region replays graphs for exactly K calls,
-bracketed by torch.cuda.synchronize().
+not pad the per-call time.  Before the W warmup steps the graphs are replayed,
+untimed, for SETTLE_S seconds so the GPU's clocks reach their steady state
+(the first ~10 ms of back-to-back calls run up to 5% slower); the timed
+region replays graphs for exactly K calls, bracketed by
+torch.cuda.synchronize().
 
 Prints ONE JSON line with the driver's fields plus
   roofline      tree-only configs: algorithmic bytes (Q+K+V+O) / kernel time
@@ -36,6 +39,7 @@ METRIC = "verify-attn µs/call + achieved HBM GB/s, b=4 d=5 N=1365 H=32 D=128 fp
 PEAK_HBM = 8.0e12     # B/s, MI355X HBM3E (vendor figure)
 PEAK_MFMA = 2.5e15    # FLOP/s, MI355X dense fp16 MFMA (vendor figure)
 CALLS_PER_GRAPH = 8
+SETTLE_S = 0.1        # untimed replays before the warmup steps (clock settling)
 
 # BASELINE.json configs[1..4]
 CONFIGS = {
@@ -231,6 +235,14 @@ def main():
         graphs.append(g)
     replays = max(1, -(-args.steps // CALLS_PER_GRAPH))
     steps = replays * CALLS_PER_GRAPH
+    t_settle = time.perf_counter()
+    k = 0
+    while time.perf_counter() - t_settle < SETTLE_S:
+        graphs[k % nsets].replay()
+        k += 1
+        if k % 8 == 0:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
     for k in range(max(1, args.warmup // CALLS_PER_GRAPH)):
         graphs[k % nsets].replay()
     torch.cuda.synchronize()
@@ -277,6 +289,7 @@ def main():
         "n_gpus": 1,
         "steps": steps,
         "warmup": args.warmup,
+        "settle_s": SETTLE_S,
         "ms_per_step": round(wall_us / 1e3, 5),
         "higher_is_better": False,
         "scaling": "weak",

@@ -643,6 +643,11 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void tree_stream_kernel(
     if (cur.valid) {
         tile_rowmap<D>(p, gdiv, cur, rm);
         tile_issue<D>(p, cur, rm, sg);
+        // the first query table is built while the first loads are in flight
+        // (the first loop top's barrier publishes it)
+        build_query_table(p, gdiv, cur, qtab);
+        tab_tile = cur.tile;
+        tab_n = cur.n;
     }
     if (dyn && leader) ans = sched_grab(grab_ctr);  // answered by the first loop top
     bool first = true;
