@@ -147,13 +147,13 @@ __device__ __forceinline__ bool tile_setup_se(const TreeParams& p, const Subtree
         return false;
     }
     const int b = p.bdiv.d;
-
     int bi = 0;
 #pragma unroll
     for (int i = 1; i < kMaxBands; ++i) bi += (tile >= plan.tile_base[i]) ? 1 : 0;
     const uint32_t bpk = plan.band[bi];
+    const int tbase = plan.tile_base[bi];
     int lo = (int)(bpk & 255u), hi = (int)((bpk >> 8) & 255u);
-    const int G = (int)(bpk >> 16), tbase = plan.tile_base[bi];
+    const int G = (int)(bpk >> 16);
     int64_t r0, r1;  // root range [r0, r1) at level lo
     if (b == 1) {
         lo = (tile - tbase) * plan.chain_h;
@@ -610,8 +610,10 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void tree_stream_kernel(
 
     const int grp = divide((int)blockIdx.x, sa.ngroups);
     const int g = (int)blockIdx.x - grp * sa.ngroups.d;  // group
-    int k = grp;                                         // current item
-    if (k >= sa.items) return;  // uniform: no barrier below is skipped by a subset of waves
+    // current item; grp < gsize <= items (the host's grid), so every workgroup
+    // has a first item and no kernel argument has to arrive before the loads
+    // below are addressed
+    int k = grp;
     const bool dyn = sa.sched != nullptr;
     uint32_t* grab_ctr = dyn ? sa.sched + (size_t)g * kSchedStride : nullptr;
     uint32_t* done_ctr = dyn ? grab_ctr + 1 : nullptr;
@@ -783,6 +785,10 @@ static int launch_stream_t(const TreeParams& p, const SubtreePlan& plan, hipStre
     sa.ngroups = make_divider((int32_t)ngroups);
     sa.gsize = (int32_t)(grid / ngroups);
     sa.items = (int32_t)(n_work / ngroups);
+    if (sa.gsize > sa.items) {  // not for this grid: every workgroup needs a first item
+        set_error("subtree launch: %d workgroups per group for %d items", sa.gsize, sa.items);
+        return QATTN_ERR_ARG;
+    }
     sa.sched = (ngroups <= kSchedGroups && sa.items > sa.gsize) ? sched_counters(dev, st) : nullptr;
     hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(kStThreads), lds, st, p, plan, sa);
     return launch_status("tree_stream_kernel");
