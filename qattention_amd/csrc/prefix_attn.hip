@@ -57,8 +57,11 @@ __global__ __launch_bounds__(kPrefixThreads) __attribute__((amdgpu_waves_per_eu(
     PrefixParams p, TreeParams tp) {
     constexpr int NC = D / 32;      // MFMA k-chunks over the head dim
     constexpr int ND = D / 16;      // output tiles over the head dim
-    constexpr int KROW = D + 8;     // Ks row stride in elements (16-byte pad)
-    constexpr int VROW = kBN + 8;   // Vt row stride in elements
+    // Row strides in elements, padded so a wave's 16-row operand reads hit
+    // distinct LDS banks: 288-byte K rows and 160-byte V^T rows read
+    // conflict-free on gfx950 (probed; 272- and 144-byte rows did not).
+    constexpr int KROW = D + 16;    // Ks row stride in elements
+    constexpr int VROW = kBN + 16;  // Vt row stride in elements
     constexpr int DV = D / 8;       // 16-byte vectors per head row
     constexpr int LDS_HALVES = kBN * KROW + D * VROW;
     __shared__ __attribute__((aligned(16))) uint16_t lds[LDS_HALVES];
@@ -187,16 +190,28 @@ __global__ __launch_bounds__(kPrefixThreads) __attribute__((amdgpu_waves_per_eu(
     auto compute_block = [&](int kb, auto mask_tag) {
         constexpr bool MASK = decltype(mask_tag)::value;
         // ---- S^T = K Q^T: lane holds keys 16 mt + 4 lq + i of query l16 ----
+        // Software-pipelined: the K operand of step i + 1 is read before the
+        // products of step i are issued; step i = (c, mt), consecutive steps
+        // accumulate into different key tiles.
         f4_t sacc[kQB][4];
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt) {
 #pragma unroll
             for (int b = 0; b < kQB; ++b) sacc[b][mt] = f4_t{0.f, 0.f, 0.f, 0.f};
+        }
+        {
+            constexpr int NS = 4 * NC;
+            Vec16 ka[2];
+            ka[0] = ld16(Ks + l16 * KROW + 8 * lq);
 #pragma unroll
-            for (int c = 0; c < NC; ++c) {
-                const Vec16 a = ld16(Ks + (16 * mt + l16) * KROW + 32 * c + 8 * lq);
+            for (int i = 0; i < NS; ++i) {
+                if (i + 1 < NS) {
+                    const int c1 = (i + 1) / 4, mt1 = (i + 1) % 4;
+                    ka[(i + 1) & 1] = ld16(Ks + (16 * mt1 + l16) * KROW + 32 * c1 + 8 * lq);
+                }
+                const int cc = i / 4, mt = i % 4;
 #pragma unroll
-                for (int b = 0; b < kQB; ++b) sacc[b][mt] = MfmaOps<T>::mma(a, qf[b][c], sacc[b][mt]);
+                for (int b = 0; b < kQB; ++b) sacc[b][mt] = MfmaOps<T>::mma(ka[i & 1], qf[b][cc], sacc[b][mt]);
             }
         }
         // ---- online softmax, per column block.  The running max is kept on
@@ -265,14 +280,21 @@ __global__ __launch_bounds__(kPrefixThreads) __attribute__((amdgpu_waves_per_eu(
             }
         }
 
-        // ---- O^T += V^T P^T, two 32-key chunks ----
+        // ---- O^T += V^T P^T, two 32-key chunks, pipelined like S: step
+        // i = (kc, dt) ----
+        {
+            constexpr int NS = 2 * ND;
+            Vec16 va[2];
+            va[0] = ld16(Vt + l16 * VROW + 8 * lq);
 #pragma unroll
-        for (int dt = 0; dt < ND; ++dt) {
+            for (int i = 0; i < NS; ++i) {
+                if (i + 1 < NS) {
+                    const int kc1 = (i + 1) / ND, dt1 = (i + 1) % ND;
+                    va[(i + 1) & 1] = ld16(Vt + (16 * dt1 + l16) * VROW + 32 * kc1 + 8 * lq);
+                }
+                const int kc = i / ND, dt = i % ND;
 #pragma unroll
-            for (int kc = 0; kc < 2; ++kc) {
-                const Vec16 a = ld16(Vt + (16 * dt + l16) * VROW + 32 * kc + 8 * lq);
-#pragma unroll
-                for (int b = 0; b < kQB; ++b) oacc[b][dt] = MfmaOps<T>::mma(a, pf[b][kc], oacc[b][dt]);
+                for (int b = 0; b < kQB; ++b) oacc[b][dt] = MfmaOps<T>::mma(va[i & 1], pf[b][kc], oacc[b][dt]);
             }
         }
     };
