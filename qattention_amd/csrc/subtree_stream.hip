@@ -110,10 +110,12 @@ __device__ __forceinline__ int tile_seq(const StreamArgs& sa, int w) {
 // node range), for a sequence spanning tokens [s, e) (cu_seqlens[seq],
 // cu_seqlens[seq + 1], wave-uniform).  Returns true when the level table was
 // (re)computed, false when it was taken from prev (same tile index and
-// sequence length).
+// sequence length).  band_tb / band_pk: lane i holds plan.tile_base[i] /
+// plan.band[i] (INT32_MAX / 0 past the bands), loaded once per workgroup.
 template <int D>
 __device__ __forceinline__ bool tile_setup_se(const TreeParams& p, const SubtreePlan& plan, const StreamArgs& sa,
-                                              int w, int32_t s, int32_t e, const TileMeta& prev, TileMeta& t) {
+                                              int w, int32_t s, int32_t e, const TileMeta& prev, TileMeta& t,
+                                              int32_t band_tb, uint32_t band_pk) {
     const int lane = threadIdx.x & 63;
     t.valid = 0;
     t.rows = t.nq = 0;
@@ -147,11 +149,10 @@ __device__ __forceinline__ bool tile_setup_se(const TreeParams& p, const Subtree
         return false;
     }
     const int b = p.bdiv.d;
-    int bi = 0;
-#pragma unroll
-    for (int i = 1; i < kMaxBands; ++i) bi += (tile >= plan.tile_base[i]) ? 1 : 0;
-    const uint32_t bpk = plan.band[bi];
-    const int tbase = plan.tile_base[bi];
+    // the tile's band: bands cover ascending tile ranges from tile 0
+    const int bi = (int)__builtin_popcountll(__ballot(tile >= band_tb)) - 1;
+    const uint32_t bpk = (uint32_t)__builtin_amdgcn_readlane((int)band_pk, bi);
+    const int tbase = __builtin_amdgcn_readlane(band_tb, bi);
     int lo = (int)(bpk & 255u), hi = (int)((bpk >> 8) & 255u);
     const int G = (int)(bpk >> 16);
     int64_t r0, r1;  // root range [r0, r1) at level lo
@@ -239,12 +240,12 @@ __device__ __forceinline__ bool tile_setup_se(const TreeParams& p, const Subtree
 template <int D>
 __device__ __forceinline__ bool tile_setup(const TreeParams& p, const SubtreePlan& plan, const StreamArgs& sa,
                                            const int32_t __attribute__((address_space(3)))* cu_lds, int w,
-                                           const TileMeta& prev, TileMeta& t) {
+                                           const TileMeta& prev, TileMeta& t, int32_t band_tb, uint32_t band_pk) {
     int seq = tile_seq(sa, w);
     seq = seq < p.B ? seq : p.B;  // tile_setup_se rejects seq >= B
     const int32_t s = __builtin_amdgcn_readfirstlane(cu_lds[seq]);
     const int32_t e = __builtin_amdgcn_readfirstlane(cu_lds[seq < p.B ? seq + 1 : seq]);
-    return tile_setup_se<D>(p, plan, sa, w, s, e, prev, t);
+    return tile_setup_se<D>(p, plan, sa, w, s, e, prev, t, band_tb, band_pk);
 }
 
 template <int D>
@@ -626,6 +627,12 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void tree_stream_kernel(
     // so it stays in one register while the request is in flight)
     uint32_t ans = 0;
     const int w = k * sa.ngroups.d + g;
+    // the plan's band table, one band per lane, from a single vector load
+    // each: the scalar lookup took two dependent kernel-argument round trips
+    // on every workgroup's first tile (~3.8 us at kernel start)
+    const int lane = threadIdx.x & 63;
+    const int32_t band_tb = lane < kMaxBands ? plan.tile_base[lane] : INT32_MAX;
+    const uint32_t band_pk = lane < kMaxBands ? plan.band[lane] : 0u;
     // V rows the PV product reads but no tile has written yet must hold finite
     // values (P = 0 multiplies them): zero them once
     for (int i = threadIdx.x; i < Geo::V_ROWS * Geo::PITCH / 8; i += kStThreads)
@@ -645,7 +652,7 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void tree_stream_kernel(
     const int32_t cu_mine = threadIdx.x <= p.B ? p.cu[threadIdx.x] : 0;  // p.B < kCuCache = kStThreads
     const int32_t s0 = __builtin_amdgcn_readfirstlane(p.cu[seq0]);
     const int32_t e0 = __builtin_amdgcn_readfirstlane(p.cu[seq0 + 1]);
-    tile_setup_se<D>(p, plan, sa, w, s0, e0, none, cur);
+    tile_setup_se<D>(p, plan, sa, w, s0, e0, none, cur, band_tb, band_pk);
     if (cur.valid) {
         tile_rowmap<D>(p, gdiv, cur, rm);
         tile_issue<D>(p, cur, rm, sg);
@@ -674,7 +681,7 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void tree_stream_kernel(
         const int wn = kn * sa.ngroups.d + g;
         TileMeta nxt;
         if (more) {
-            const bool fresh = tile_setup<D>(p, plan, sa, cu_lds, wn, cur, nxt);
+            const bool fresh = tile_setup<D>(p, plan, sa, cu_lds, wn, cur, nxt, band_tb, band_pk);
             if (nxt.valid) {
                 if (fresh) tile_rowmap<D>(p, gdiv, nxt, rm);
                 tile_issue<D>(p, nxt, rm, sg);
