@@ -634,9 +634,15 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void tree_stream_kernel(
     const int32_t band_tb = lane < kMaxBands ? plan.tile_base[lane] : INT32_MAX;
     const uint32_t band_pk = lane < kMaxBands ? plan.band[lane] : 0u;
     // V rows the PV product reads but no tile has written yet must hold finite
-    // values (P = 0 multiplies them): zero them once
-    for (int i = threadIdx.x; i < Geo::V_ROWS * Geo::PITCH / 8; i += kStThreads)
-        st16(Vs + 8 * i, Vec16{{0u, 0u, 0u, 0u}});
+    // values (P = 0 multiplies them): zero them once.  Each thread zeroes the
+    // V chunks it stages itself, so its own tile stores follow the zeros in
+    // program order (the first loop top's barrier publishes both).
+    {
+        const int rsub = threadIdx.x / Geo::CPR, c = threadIdx.x % Geo::CPR;
+#pragma unroll
+        for (int ps = 0; ps < Geo::PASSES; ++ps)
+            st16(Vs + (ps * Geo::RPP + rsub) * Geo::PITCH + 8 * c, Vec16{{0u, 0u, 0u, 0u}});
+    }
     const int32_t __attribute__((address_space(3)))* cu_lds =
         (const int32_t __attribute__((address_space(3)))*)cuc;
 
