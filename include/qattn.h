@@ -4,8 +4,19 @@
  *
  * Every entry point takes plain device pointers, element strides and sizes,
  * launches asynchronously on the given HIP stream (hipStream_t passed as
- * void*, NULL = the legacy default stream), allocates nothing and keeps no
- * global mutable state, so calls are reentrant and HIP-graph capturable.
+ * void*, NULL = the legacy default stream) and is HIP-graph capturable.
+ * Outputs and workspaces belong to the caller.  The library's one allocation
+ * is a 2 MiB pool of work-schedule counters per device, allocated and zeroed
+ * (synchronously) by the first uncaptured call that launches the subtree
+ * kernel on that device, and kept until the process ends; every launch
+ * leaves its counters at zero.  Uncaptured launches take the pool's 32 eager
+ * slots in turn, so up to 32 of them may be in flight at once per device
+ * (on different streams).  A launch recorded into a graph keeps a slot of
+ * its own, 96 per device per process; past that, or while the first call on
+ * a device is being recorded, recorded launches use a static schedule (same
+ * results, slower).  Two graph executables instantiated from one capture
+ * share its slots and must not run at the same time.  Calls are
+ * thread-safe (the pool is guarded by a mutex).
  * Return value: QATTN_OK (0) or a negative QATTN_ERR_* code; the message of
  * the last failure on the calling thread is qattn_last_error().
  *

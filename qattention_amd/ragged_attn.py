@@ -5,8 +5,10 @@ src/ragged_attn.py (saifmb0/QAttention).  Names, argument order, defaults,
 return values and error behaviour follow the reference; the work is done by
 hand-written gfx950 HIP kernels in libqattn.so, called through its C ABI
 (include/qattn.h) on torch's current HIP stream.  Outputs are allocated here
-through the torch caching allocator, so a call allocates nothing inside the
-library and is HIP-graph capturable when max_seqlen is given (no host sync).
+through the torch caching allocator.  A call is HIP-graph capturable when
+max_seqlen is given (no host sync); inside the library the only allocation is
+a per-device pool of work-schedule counters, made by the first uncaptured call
+that launches the subtree kernel on a device.
 
 Differences from the reference, all supersets:
   * K/V may carry fewer heads than Q (GQA): q head h reads kv head
