@@ -52,21 +52,40 @@ struct PrefixParams {
     float scale_log2;
 };
 
+// 16-byte chunk swizzle of the K/V blocks in LDS: chunk c of key row r sits at
+// position c ^ kv_swz(r) of its (unpadded) row.  With 256-byte rows both
+// operand reads are bank-conflict free on gfx950 (probed with
+// SQ_LDS_BANK_CONFLICT): the K reads (ds_read_b128, rows 16 mt + l16, chunk
+// 4 c + lq) and the V^T reads (ds_read_b64_tr_b16, 8 rows of 32 bytes per
+// 32-lane pass).  Smaller head dims keep the low bits (correct, not probed).
+__device__ __forceinline__ int kv_swz(int r, int dv) {
+    const int b2 = (r >> 2) & 1, b3 = (r >> 3) & 1;
+    return ((2 * (r & 3)) | (8 * (b3 ^ b2)) | b2) & (dv - 1);
+}
+
+// s_waitcnt immediate (gfx9 encoding): vmcnt N, expcnt and lgkmcnt unconstrained
+constexpr int kWaitVm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+
 template <typename T, int D, bool FUSED, bool LSE>
 __global__ __launch_bounds__(kPrefixThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefix_attn_kernel(
     PrefixParams p, TreeParams tp) {
     constexpr int NC = D / 32;      // MFMA k-chunks over the head dim
     constexpr int ND = D / 16;      // output tiles over the head dim
-    // Row strides in elements, padded so a wave's 16-row operand reads hit
-    // distinct LDS banks: 288-byte K rows and 160-byte V^T rows read
-    // conflict-free on gfx950 (probed; 272- and 144-byte rows did not).
-    constexpr int KROW = D + 16;    // Ks row stride in elements
-    constexpr int VROW = kBN + 16;  // Vt row stride in elements
-    constexpr int DV = D / 8;       // 16-byte vectors per head row
-    constexpr int LDS_HALVES = kBN * KROW + D * VROW;
-    __shared__ __attribute__((aligned(16))) uint16_t lds[LDS_HALVES];
-    uint16_t* Ks = lds;
-    uint16_t* Vt = lds + kBN * KROW;
+    constexpr int DV = D / 8;       // 16-byte chunks per key row
+    constexpr int BLK = kBN * D;    // elements of one K or V block
+    constexpr int NI = D / 32;      // 1 KB LDS loads per thread per K (or V) block
+    constexpr int RPI = 512 / D;    // key rows per 1 KB load
+    static_assert(NI * 4 * 512 == BLK, "a block is 4 waves x NI loads of 1 KB");
+    // Double buffers of the K and V blocks, four LDS variables so that the
+    // compiler tells them apart: a read of one buffer does not wait for the
+    // LDS-DMA loads in flight into another.
+    __shared__ __attribute__((aligned(1024))) uint16_t Kb0[BLK], Kb1[BLK], Vb0[BLK], Vb1[BLK];
+    auto kbuf = [&](auto i) -> uint16_t* {
+        if constexpr (decltype(i)::value == 0) return Kb0; else return Kb1;
+    };
+    auto vbuf = [&](auto i) -> uint16_t* {
+        if constexpr (decltype(i)::value == 0) return Vb0; else return Vb1;
+    };
 
     // Logical unit order puts the query tiles of one (sequence, kv head, split)
     // next to each other; hardware deals blockIdx round-robin over the 8 XCDs,
@@ -96,29 +115,34 @@ __global__ __launch_bounds__(kPrefixThreads) __attribute__((amdgpu_waves_per_eu(
     const int lq = lane >> 4;
 
     // this lane's query rows (B operand column / output column), one per block
-    int64_t qrow[kQB];
-    int qh[kQB];
-    bool rvalid[kQB];
+    // (token row, q head) of this lane's query in column block b (recomputed
+    // after the key loop rather than kept live through it)
+    auto query_of = [&](int b, int64_t& qrow, int& qh) {
+        const int rr = qt * kBM + wave * (16 * kQB) + 16 * b + l16;
+        const int tok = divide(rr, p.gdiv);
+        qh = kvh * g + (rr - tok * g);
+        qrow = (int64_t)s0 + tok;
+        return rr < rows;
+    };
     Vec16 qf[kQB][NC];
 #pragma unroll
     for (int b = 0; b < kQB; ++b) {
-        const int rr = qt * kBM + wave * (16 * kQB) + 16 * b + l16;
-        rvalid[b] = rr < rows;
-        const int tok = rvalid[b] ? divide(rr, p.gdiv) : 0;
-        qh[b] = kvh * g + (rr - divide(rr, p.gdiv) * g);
-        qrow[b] = (int64_t)s0 + tok;
+        int64_t qrow;
+        int qh;
+        const bool valid = query_of(b, qrow, qh);
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
             qf[b][c] = Vec16{{0u, 0u, 0u, 0u}};
-            if (rvalid[b])
-                qf[b][c] = ld16((const uint16_t*)p.q + qrow[b] * p.sq_t + (int64_t)qh[b] * p.sq_h + 32 * c + 8 * lq);
+            if (valid) qf[b][c] = ld16((const uint16_t*)p.q + qrow * p.sq_t + (int64_t)qh * p.sq_h + 32 * c + 8 * lq);
         }
     }
 
     const int k_lo = split * p.blocks_per_split * kBN;
     const int k_hi = (k_lo + p.blocks_per_split * kBN < p.L) ? k_lo + p.blocks_per_split * kBN : p.L;
-    const uint16_t* kbase = (const uint16_t*)p.kp + (int64_t)seq * p.skp_b + (int64_t)kvh * p.skp_h;
-    const uint16_t* vbase = (const uint16_t*)p.vp + (int64_t)seq * p.svp_b + (int64_t)kvh * p.svp_h;
+    const int nb = (k_hi - k_lo + kBN - 1) / kBN;  // >= 1: every split holds a key
+    const char* kbase = (const char*)((const uint16_t*)p.kp + (int64_t)seq * p.skp_b + (int64_t)kvh * p.skp_h);
+    const char* vbase = (const char*)((const uint16_t*)p.vp + (int64_t)seq * p.svp_b + (int64_t)kvh * p.svp_h);
+    const int64_t kst = 2 * p.skp_t, vst = 2 * p.svp_t;  // bytes between keys
 
     float m_run[kQB], l_run[kQB];
     f4_t oacc[kQB][ND];
@@ -130,94 +154,98 @@ __global__ __launch_bounds__(kPrefixThreads) __attribute__((amdgpu_waves_per_eu(
         for (int i = 0; i < ND; ++i) oacc[b][i] = f4_t{0.f, 0.f, 0.f, 0.f};
     }
 
-    // ---- K/V block staging, software-pipelined through registers: the loads
-    // of block i+1 are issued right after block i is in LDS and land while the
-    // MFMAs of block i run ----
-    constexpr int KU = kBN * DV / kPrefixThreads;                        // K vectors per thread
-    constexpr int VUNITS = (kBN / 4) * DV;                                // 4-key x 8-dim V units
-    constexpr int VU = (VUNITS + kPrefixThreads - 1) / kPrefixThreads;   // V units per thread
-    static_assert((kBN * DV) % kPrefixThreads == 0 && (VUNITS % 64) == 0, "staging must tile whole waves");
-    Vec16 kreg[KU], vreg[VU][4];
-    // Keys of the tail block beyond k_hi load row k_hi - 1 instead (always
-    // inside the split); their scores are masked to -inf, so P = 0 there.
-    auto load_block = [&](int kb) {
+    // ---- K/V blocks go straight from global memory to LDS (global_load_lds,
+    // 16 bytes per lane, lane i of a load writes bytes [16 i, 16 i + 16) of its
+    // 1 KB): load i of wave w covers key rows (w NI + i) RPI .. + RPI - 1, and
+    // each lane fetches the chunk that the swizzle puts at its position ----
+    // Byte offsets of this lane's loads within a block: 32-bit (the host checks
+    // that 64 key rows span less than 4 GB), added to the block's uniform base.
+    uint32_t koff[NI], voff[NI];
 #pragma unroll
-        for (int i = 0; i < KU; ++i) {
-            const int u = tid + i * kPrefixThreads;
-            const int key = min(kb + u / DV, k_hi - 1), ch = u % DV;
-            kreg[i] = ld16(kbase + (int64_t)key * p.skp_t + 8 * ch);
-        }
+    for (int i = 0; i < NI; ++i) {
+        const int row = (wave * NI + i) * RPI + lane / DV;
+        const uint32_t col = 16 * ((lane % DV) ^ kv_swz(row, DV));
+        koff[i] = (uint32_t)row * (uint32_t)kst + col;
+        voff[i] = (uint32_t)row * (uint32_t)vst + col;
+    }
+    auto issue = [&](const char* base, int64_t st, const uint32_t (&off)[NI], int j, uint16_t* buf) {
+        const int kb = k_lo + j * kBN;
+        const char* gb = base + (int64_t)kb * st;
+        if (kb + kBN <= k_hi) {
 #pragma unroll
-        for (int i = 0; i < VU; ++i) {
-            const int u = tid + i * kPrefixThreads;
-            const int kg = u % (kBN / 4), dch = u / (kBN / 4);
+            for (int i = 0; i < NI; ++i)
+                __builtin_amdgcn_global_load_lds(
+                    (const void*)(gb + off[i]), (__attribute__((address_space(3))) void*)(buf + (wave * NI + i) * 512),
+                    16, 0, 0);
+        } else {
+            // tail block of the split: rows past k_hi - 1 load that key instead
+            const int last = k_hi - 1 - kb;
 #pragma unroll
-            for (int rk = 0; rk < 4; ++rk) {
-                const int key = min(kb + 4 * kg + rk, k_hi - 1);
-                if (u < VUNITS) vreg[i][rk] = ld16(vbase + (int64_t)key * p.svp_t + 8 * dch);  // wave-uniform
+            for (int i = 0; i < NI; ++i) {
+                const int row = (wave * NI + i) * RPI + lane / DV;
+                const uint32_t col = 16 * ((lane % DV) ^ kv_swz(row, DV));
+                __builtin_amdgcn_global_load_lds(
+                    (const void*)(gb + (uint32_t)min(row, last) * (uint32_t)st + col),
+                    (__attribute__((address_space(3))) void*)(buf + (wave * NI + i) * 512), 16, 0, 0);
             }
         }
     };
-    auto store_block = [&]() {
+    auto issue_k = [&](int j, auto buf) { issue(kbase, kst, koff, j, kbuf(buf)); };
+    auto issue_v = [&](int j, auto buf) { issue(vbase, vst, voff, j, vbuf(buf)); };
+
+    // operand read addresses (elements): K row 16 mt + l16, chunk 4 c + lq;
+    // V^T through ds_read_b64_tr_b16: lane j of 16-lane group lq reads key row
+    // 32 kc + 16 h + 4 lq + j / 4 at dims 16 dt + 4 (j % 4) .. + 3, and receives
+    // keys 32 kc + 16 h + 4 lq + 0..3 at dim 16 dt + j -- the key order of the
+    // P^T operand formed from the S^T output registers.  The V^T address of
+    // d-tile dt is vaddr0 ^ (16 dt): the swizzle flips only chunk bits, which
+    // the row base leaves clear.
+    int kaddr[NC];
+    int vaddr0;
+    {
+        const int sk = kv_swz(l16, DV);
 #pragma unroll
-        for (int i = 0; i < KU; ++i) {
-            const int u = tid + i * kPrefixThreads;
-            st16(Ks + (u / DV) * KROW + 8 * (u % DV), kreg[i]);
-        }
+        for (int c = 0; c < NC; ++c) kaddr[c] = l16 * D + 8 * ((4 * c + lq) ^ sk);
+        const int vr = 4 * lq + (l16 >> 2);
+        vaddr0 = vr * D + 8 * (((l16 & 3) >> 1) ^ kv_swz(vr, DV)) + 4 * (l16 & 1);
+    }
+
+    // S^T = K Q^T of the block in K buffer kbuf: lane holds keys 16 mt + 4 lq + i
+    // of query l16.  Step i = (c, mt); the K operand of step i + 1 is read
+    // before the products of step i are issued.
+    auto s_product = [&](auto buf, f4_t (&s)[kQB][4]) {
+        const uint16_t* kb = kbuf(buf);
 #pragma unroll
-        for (int i = 0; i < VU; ++i) {
-            const int u = tid + i * kPrefixThreads;
-            if (u >= VUNITS) continue;
-            const int kg = u % (kBN / 4), dch = u / (kBN / 4);
-            const int col = vt_col(4 * kg);
-            const Vec16* v4 = vreg[i];
+        for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-            for (int m = 0; m < 4; ++m) {
-                // d = 8 dch + 2m (low halves) and 8 dch + 2m + 1 (high halves)
-                const uint32_t e01 = __builtin_amdgcn_perm(v4[1].w[m], v4[0].w[m], 0x05040100u);
-                const uint32_t e23 = __builtin_amdgcn_perm(v4[3].w[m], v4[2].w[m], 0x05040100u);
-                const uint32_t o01 = __builtin_amdgcn_perm(v4[1].w[m], v4[0].w[m], 0x07060302u);
-                const uint32_t o23 = __builtin_amdgcn_perm(v4[3].w[m], v4[2].w[m], 0x07060302u);
-                *reinterpret_cast<uint2*>(Vt + (8 * dch + 2 * m) * VROW + col) = make_uint2(e01, e23);
-                *reinterpret_cast<uint2*>(Vt + (8 * dch + 2 * m + 1) * VROW + col) = make_uint2(o01, o23);
+            for (int b = 0; b < kQB; ++b) s[b][mt] = f4_t{0.f, 0.f, 0.f, 0.f};
+        constexpr int NS = 4 * NC;
+        Vec16 ka[2];
+        ka[0] = ld16(kb + kaddr[0]);
+#pragma unroll
+        for (int i = 0; i < NS; ++i) {
+            if (i + 1 < NS) {
+                const int c1 = (i + 1) / 4, mt1 = (i + 1) % 4;
+                ka[(i + 1) & 1] = ld16(kb + kaddr[c1] + 16 * D * mt1);
             }
+            const int cc = i / 4, mt = i % 4;
+#pragma unroll
+            for (int b = 0; b < kQB; ++b) s[b][mt] = MfmaOps<T>::mma(ka[i & 1], qf[b][cc], s[b][mt]);
         }
     };
 
-    if (k_lo < k_hi) load_block(k_lo);
-    // One 64-key block from LDS; MASK instantiates the split's tail block, the
-    // only one with keys beyond k_hi, so full blocks carry no masking code.
-    auto compute_block = [&](int kb, auto mask_tag) {
+    // Online softmax of one block, per column block.  The running max is kept
+    // on raw scores q.k (scale > 0 keeps the order) and scale*log2(e) is folded
+    // into the exponent: p = exp2(s c - m c), one FMA.  Lazy rescaling: the
+    // exponent reference m_run only moves when a block max exceeds it by more
+    // than kLazy/c (a factor 2^kLazy in P), so the accumulators are rescaled on
+    // a handful of blocks.  P stays <= 2^kLazy (exact in fp16/bf16 range, same
+    // relative precision) and l carries the same reference.
+    const float csc = p.scale_log2;
+    auto softmax = [&](f4_t (&s)[kQB][4], Vec16 (&pf)[kQB][2], float (&alpha)[kQB], bool& rescale, int kb,
+                       auto mask_tag) {
         constexpr bool MASK = decltype(mask_tag)::value;
-        // ---- S^T = K Q^T: lane holds keys 16 mt + 4 lq + i of query l16 ----
-        // Software-pipelined: the K operand of step i + 1 is read before the
-        // products of step i are issued; step i = (c, mt), consecutive steps
-        // accumulate into different key tiles.
-        f4_t sacc[kQB][4];
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
-#pragma unroll
-            for (int b = 0; b < kQB; ++b) sacc[b][mt] = f4_t{0.f, 0.f, 0.f, 0.f};
-        }
-        {
-            constexpr int NS = 4 * NC;
-            Vec16 ka[2];
-            ka[0] = ld16(Ks + l16 * KROW + 8 * lq);
-#pragma unroll
-            for (int i = 0; i < NS; ++i) {
-                if (i + 1 < NS) {
-                    const int c1 = (i + 1) / 4, mt1 = (i + 1) % 4;
-                    ka[(i + 1) & 1] = ld16(Ks + (16 * mt1 + l16) * KROW + 32 * c1 + 8 * lq);
-                }
-                const int cc = i / 4, mt = i % 4;
-#pragma unroll
-                for (int b = 0; b < kQB; ++b) sacc[b][mt] = MfmaOps<T>::mma(ka[i & 1], qf[b][cc], sacc[b][mt]);
-            }
-        }
-        // ---- online softmax, per column block.  The running max is kept on
-        // raw scores q.k (scale > 0 keeps the order) and the scale*log2(e)
-        // factor is folded into the exponent: p = exp2(s c - m c), one FMA ----
-        const float c = p.scale_log2;
+        constexpr float kLazy = 8.f;
         if constexpr (MASK) {  // tail block of the split: keys at or beyond k_hi do not exist
 #pragma unroll
             for (int b = 0; b < kQB; ++b)
@@ -225,39 +253,28 @@ __global__ __launch_bounds__(kPrefixThreads) __attribute__((amdgpu_waves_per_eu(
                 for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
                     for (int i = 0; i < 4; ++i)
-                        if (kb + 16 * mt + 4 * lq + i >= k_hi) sacc[b][mt][i] = -INFINITY;
+                        if (kb + 16 * mt + 4 * lq + i >= k_hi) s[b][mt][i] = -INFINITY;
         }
-        // Lazy rescaling: the exponent reference m_run only moves when a block
-        // max exceeds it by more than kLazy/c (a factor 2^kLazy in P), so the
-        // accumulators are rescaled on a handful of blocks instead of nearly
-        // every block.  P stays <= 2^kLazy (exact in fp16/bf16 range, same
-        // relative precision) and l carries the same reference, so the final
-        // normalisation is unchanged.
-        constexpr float kLazy = 8.f;
-        Vec16 pf[kQB][2];
-        bool rescale = false;
-        float alpha[kQB];
 #pragma unroll
         for (int b = 0; b < kQB; ++b) {
             float mb = -INFINITY;
 #pragma unroll
             for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) mb = fmaxf(mb, sacc[b][mt][i]);
-            mb = xor_max(mb, 16);
-            mb = xor_max(mb, 32);
-            const bool move = (mb - m_run[b]) * c > kLazy;  // always true on the first block
+                for (int i = 0; i < 4; ++i) mb = fmaxf(mb, s[b][mt][i]);
+            mb = col4_max(mb);
+            const bool move = (mb - m_run[b]) * csc > kLazy;  // always true on the first block
             const float m_new = move ? mb : m_run[b];
-            alpha[b] = move ? fast_exp2((m_run[b] - m_new) * c) : 1.f;  // m_run = -inf: 0
+            alpha[b] = move ? fast_exp2((m_run[b] - m_new) * csc) : 1.f;  // m_run = -inf: 0
             rescale |= move;
-            const float mc = m_new * c;
+            const float mc = m_new * csc;
             float psum = 0.f;
 #pragma unroll
             for (int mt = 0; mt < 4; ++mt) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const float e = fast_exp2(__builtin_fmaf(sacc[b][mt][i], c, -mc));
-                    sacc[b][mt][i] = e;
+                    const float e = fast_exp2(__builtin_fmaf(s[b][mt][i], csc, -mc));
+                    s[b][mt][i] = e;
                     psum += e;
                 }
             }
@@ -265,62 +282,116 @@ __global__ __launch_bounds__(kPrefixThreads) __attribute__((amdgpu_waves_per_eu(
             m_run[b] = m_new;
 #pragma unroll
             for (int kc = 0; kc < 2; ++kc) {
-                pf[b][kc].w[0] = MfmaOps<T>::pack2(sacc[b][2 * kc][0], sacc[b][2 * kc][1]);
-                pf[b][kc].w[1] = MfmaOps<T>::pack2(sacc[b][2 * kc][2], sacc[b][2 * kc][3]);
-                pf[b][kc].w[2] = MfmaOps<T>::pack2(sacc[b][2 * kc + 1][0], sacc[b][2 * kc + 1][1]);
-                pf[b][kc].w[3] = MfmaOps<T>::pack2(sacc[b][2 * kc + 1][2], sacc[b][2 * kc + 1][3]);
-            }
-        }
-        // the accumulators need rescaling only when some running max moved
-        if (__builtin_expect(__any(rescale), 0)) {
-#pragma unroll
-            for (int b = 0; b < kQB; ++b) {
-#pragma unroll
-                for (int dt = 0; dt < ND; ++dt) oacc[b][dt] *= alpha[b];
-            }
-        }
-
-        // ---- O^T += V^T P^T, two 32-key chunks, pipelined like S: step
-        // i = (kc, dt) ----
-        {
-            constexpr int NS = 2 * ND;
-            Vec16 va[2];
-            va[0] = ld16(Vt + l16 * VROW + 8 * lq);
-#pragma unroll
-            for (int i = 0; i < NS; ++i) {
-                if (i + 1 < NS) {
-                    const int kc1 = (i + 1) / ND, dt1 = (i + 1) % ND;
-                    va[(i + 1) & 1] = ld16(Vt + (16 * dt1 + l16) * VROW + 32 * kc1 + 8 * lq);
-                }
-                const int kc = i / ND, dt = i % ND;
-#pragma unroll
-                for (int b = 0; b < kQB; ++b) oacc[b][dt] = MfmaOps<T>::mma(va[i & 1], pf[b][kc], oacc[b][dt]);
+                pf[b][kc].w[0] = MfmaOps<T>::pack2(s[b][2 * kc][0], s[b][2 * kc][1]);
+                pf[b][kc].w[1] = MfmaOps<T>::pack2(s[b][2 * kc][2], s[b][2 * kc][3]);
+                pf[b][kc].w[2] = MfmaOps<T>::pack2(s[b][2 * kc + 1][0], s[b][2 * kc + 1][1]);
+                pf[b][kc].w[3] = MfmaOps<T>::pack2(s[b][2 * kc + 1][2], s[b][2 * kc + 1][3]);
             }
         }
     };
+    auto rescale_o = [&](const float (&alpha)[kQB], bool rescale) {
+        // the accumulators need rescaling only when some running max moved
+        if (__builtin_expect(__any(rescale), 0)) {
+#pragma unroll
+            for (int b = 0; b < kQB; ++b)
+#pragma unroll
+                for (int dt = 0; dt < ND; ++dt) oacc[b][dt] *= alpha[b];
+        }
+    };
 
-    // Full blocks in the loop, the split's partial tail block peeled after it,
-    // so the loop body is one straight-line copy of compute_block.
-    int kb = k_lo;
-    for (; kb + kBN <= k_hi; kb += kBN) {
-        store_block();
-        __syncthreads();
-        if (kb + kBN < k_hi) load_block(kb + kBN);
-        compute_block(kb, std::false_type{});
-        __syncthreads();
+    // O^T += V^T P^T of the block in V buffer vbuf, two 32-key chunks; step
+    // i = (kc, dt), operands read one step ahead
+    auto pv_product = [&](auto buf, const Vec16 (&pf)[kQB][2]) {
+        typedef short v4s __attribute__((ext_vector_type(4)));
+        const uint16_t* vb = vbuf(buf);
+        auto fetch = [&](int i) {
+            const int kc = i / ND, dt = i % ND;
+            const uint16_t* a = vb + (vaddr0 ^ (16 * dt)) + 32 * D * kc;
+            const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s*)a);
+            const v4s hi =
+                __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s*)(a + 16 * D));
+            const uint2 l2 = __builtin_bit_cast(uint2, lo), h2 = __builtin_bit_cast(uint2, hi);
+            return Vec16{{l2.x, l2.y, h2.x, h2.y}};
+        };
+        constexpr int NS = 2 * ND;
+        Vec16 va[2];
+        va[0] = fetch(0);
+#pragma unroll
+        for (int i = 0; i < NS; ++i) {
+            if (i + 1 < NS) va[(i + 1) & 1] = fetch(i + 1);
+            const int kc = i / ND, dt = i % ND;
+#pragma unroll
+            for (int b = 0; b < kQB; ++b) oacc[b][dt] = MfmaOps<T>::mma(va[i & 1], pf[b][kc], oacc[b][dt]);
+        }
+    };
+
+    // ---- pipeline over the split's blocks j = 0 .. nb-1: iteration j starts
+    // after a barrier that publishes K_{j+1} and V_j, issues V_{j+1} and
+    // K_{j+2} into the buffers freed by the barrier, forms S_{j+1} on the
+    // matrix cores while the softmax of block j runs on the vector ALUs, and
+    // ends with the PV product of block j ----
+    using B0 = std::integral_constant<int, 0>;
+    using B1 = std::integral_constant<int, 1>;
+    issue_k(0, B0{});
+    issue_v(0, B0{});
+    if (nb > 1) {
+        issue_k(1, B1{});
+        __builtin_amdgcn_s_waitcnt(kWaitVm(NI));  // K_0 and V_0 (and Q) have landed
+    } else {
+        __builtin_amdgcn_s_waitcnt(kWaitVm(0));
     }
-    if (kb < k_hi) {
-        store_block();
+    __syncthreads();
+    f4_t sc[kQB][4];
+    s_product(B0{}, sc);
+    // block j uses K buffer j & 1 and V buffer j & 1; the loop is unrolled by
+    // two so every buffer choice is a compile-time constant
+    auto step = [&](int j, auto par) {
+        constexpr int P = decltype(par)::value;
+        using Pn = std::integral_constant<int, P ^ 1>;
+        __builtin_amdgcn_s_waitcnt(kWaitVm(0));
         __syncthreads();
-        compute_block(kb, std::true_type{});
-        __syncthreads();
+        issue_v(j + 1, Pn{});
+        if (j + 2 < nb) issue_k(j + 2, par);
+        f4_t sn[kQB][4];
+        Vec16 pf[kQB][2];
+        float alpha[kQB];
+        bool rescale = false;
+        softmax(sc, pf, alpha, rescale, k_lo + j * kBN, std::false_type{});
+        s_product(Pn{}, sn);
+        rescale_o(alpha, rescale);
+        pv_product(par, pf);
+#pragma unroll
+        for (int b = 0; b < kQB; ++b)
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) sc[b][mt] = sn[b][mt];
+    };
+    for (int j = 0; j + 1 < nb; j += 2) {
+        step(j, B0{});
+        if (j + 2 < nb) step(j + 1, B1{});
     }
+    {
+        __builtin_amdgcn_s_waitcnt(kWaitVm(0));
+        __syncthreads();
+        const int kb = k_lo + (nb - 1) * kBN;
+        Vec16 pf[kQB][2];
+        float alpha[kQB];
+        bool rescale = false;
+        if (kb + kBN > k_hi)
+            softmax(sc, pf, alpha, rescale, kb, std::true_type{});
+        else
+            softmax(sc, pf, alpha, rescale, kb, std::false_type{});
+        rescale_o(alpha, rescale);
+        if ((nb - 1) & 1)
+            pv_product(B1{}, pf);
+        else
+            pv_product(B0{}, pf);
+    }
+    __syncthreads();  // the LDS is reused by the fused epilogue
 
     float l_tot[kQB];
 #pragma unroll
     for (int b = 0; b < kQB; ++b) {
-        l_tot[b] = l_run[b] + __shfl_xor(l_run[b], 16);
-        l_tot[b] += __shfl_xor(l_tot[b], 32);
+        l_tot[b] = col4_sum(l_run[b]);
         m_run[b] *= p.scale_log2;  // to the log2 units of the tree walk's scores
     }
 
@@ -329,8 +400,10 @@ __global__ __launch_bounds__(kPrefixThreads) __attribute__((amdgpu_waves_per_eu(
         const int64_t plane = p.total_tokens * (int64_t)p.Hq;
 #pragma unroll
         for (int b = 0; b < kQB; ++b) {
-            if (!rvalid[b]) continue;
-            const int64_t idx = (int64_t)split * plane + qrow[b] * p.Hq + qh[b];
+            int64_t qrow;
+            int qh;
+            if (!query_of(b, qrow, qh)) continue;
+            const int64_t idx = (int64_t)split * plane + qrow * p.Hq + qh;
             if (lq == 0) {
                 p.part_m[idx] = m_run[b];
                 p.part_l[idx] = l_tot[b];
@@ -345,9 +418,11 @@ __global__ __launch_bounds__(kPrefixThreads) __attribute__((amdgpu_waves_per_eu(
         // ---- fused epilogue: re-lay each 16-row block in LDS as 4 lanes per
         // query and run the ancestor walk from this state ----
         constexpr int OROW = D + 4;  // fp32 row stride (pad)
-        float* Os = reinterpret_cast<float*>(lds) + wave * 16 * OROW;
-        float* Ms = reinterpret_cast<float*>(lds) + 4 * 16 * OROW + wave * 32;
-        static_assert((4 * 16 * OROW + 4 * 32) * 4 <= LDS_HALVES * 2, "epilogue staging must fit the LDS");
+        // each wave stages its 16-row blocks in one of the four K/V buffers
+        uint16_t* wbuf = wave == 0 ? Kb0 : (wave == 1 ? Kb1 : (wave == 2 ? Vb0 : Vb1));
+        float* Os = reinterpret_cast<float*>(wbuf);
+        float* Ms = Os + 16 * OROW;
+        static_assert((16 * OROW + 32) * 4 <= BLK * 2, "epilogue staging must fit one K/V buffer");
         const int grp = lane >> 2, j = lane & 3;
         constexpr int NCH = D / 32;
 #pragma unroll
@@ -497,6 +572,12 @@ int qattn_prefix_tree_fwd(const void* q, const int64_t q_stride[3], const void* 
     if (((uintptr_t)k_prefix & 15) || ((uintptr_t)v_prefix & 15) || kp_stride[1] % 8 || kp_stride[2] % 8 ||
         vp_stride[1] % 8 || vp_stride[2] % 8 || kp_stride[0] % 8 || vp_stride[0] % 8) {
         set_error("prefix rows must be 16-byte aligned (strides in multiples of 8 elements)");
+        return QATTN_ERR_LAYOUT;
+    }
+    // the kernel addresses a 64-key block with 32-bit byte offsets
+    if (kp_stride[1] < 0 || vp_stride[1] < 0 ||
+        (int64_t)kBN * std::max(kp_stride[1], vp_stride[1]) * 2 >= (int64_t(1) << 32)) {
+        set_error("prefix token strides must be non-negative and below 2^25 elements");
         return QATTN_ERR_LAYOUT;
     }
     const int g = num_q_heads / num_kv_heads;
