@@ -55,39 +55,69 @@ __device__ __forceinline__ void load_q4(const TreeParams& p, int64_t qrow, int h
 }
 
 // Initial state from split-K prefix partials (flash-decoding merge of all
-// splits): m = max_s m_s, l = sum_s 2^(m_s - m) l_s, acc likewise.
+// splits): m = max_s m_s, l = sum_s 2^(m_s - m) l_s, acc likewise.  The loads
+// of several splits are issued together (8 maxima, then 16 float4 of partial
+// numerators per step), so a merge of n splits waits on about n / 8 + n / SP
+// memory round trips rather than 2 n.
 template <int D>
 __device__ __forceinline__ void load_partial_state4(const TreeParams& p, int64_t qrow, int h, int j,
                                                     float& m, float& l, float* acc) {
     constexpr int NCH = D / 32;
+    constexpr int SP = 8 / NCH;  // splits per step of the weighted sum
+    const int ns = p.n_split;
     const int64_t plane = p.total_tokens * (int64_t)p.Hq;
     const int64_t idx = qrow * p.Hq + h;
     float m0 = -INFINITY;
-    for (int s = 0; s < p.n_split; ++s) m0 = fmaxf(m0, p.part_m[s * plane + idx]);
+    for (int s0 = 0; s0 < ns; s0 += 8) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = s0 + u < ns ? p.part_m[(s0 + u) * plane + idx] : -INFINITY;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) m0 = fmaxf(m0, v[u]);
+    }
     m = m0;
     l = 0.f;
 #pragma unroll
     for (int e = 0; e < 8 * NCH; ++e) acc[e] = 0.f;
     if (m0 == -INFINITY) return;
-    for (int s = 0; s < p.n_split; ++s) {
-        const float ms = p.part_m[s * plane + idx];
-        if (ms == -INFINITY) continue;
-        const float w = fast_exp2(ms - m0);
-        l = __builtin_fmaf(w, p.part_l[s * plane + idx], l);
-        const float* a = p.part_acc + (s * plane + idx) * D + 8 * j;
+    for (int s0 = 0; s0 < ns; s0 += SP) {
+        float ms[SP], ls[SP];
+        float4 a[SP][2 * NCH];
 #pragma unroll
-        for (int i = 0; i < NCH; ++i) {
-            const float4 a0 = *reinterpret_cast<const float4*>(a + 32 * i);
-            const float4 a1 = *reinterpret_cast<const float4*>(a + 32 * i + 4);
-            float* c = acc + 8 * i;
-            c[0] = __builtin_fmaf(w, a0.x, c[0]);
-            c[1] = __builtin_fmaf(w, a0.y, c[1]);
-            c[2] = __builtin_fmaf(w, a0.z, c[2]);
-            c[3] = __builtin_fmaf(w, a0.w, c[3]);
-            c[4] = __builtin_fmaf(w, a1.x, c[4]);
-            c[5] = __builtin_fmaf(w, a1.y, c[5]);
-            c[6] = __builtin_fmaf(w, a1.z, c[6]);
-            c[7] = __builtin_fmaf(w, a1.w, c[7]);
+        for (int u = 0; u < SP; ++u) {
+            ms[u] = -INFINITY;
+            ls[u] = 0.f;
+#pragma unroll
+            for (int i = 0; i < 2 * NCH; ++i) a[u][i] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (s0 + u < ns) {  // wave-uniform
+                const int64_t k = (s0 + u) * plane + idx;
+                ms[u] = p.part_m[k];
+                ls[u] = p.part_l[k];
+                const float* src = p.part_acc + k * D + 8 * j;
+#pragma unroll
+                for (int i = 0; i < NCH; ++i) {
+                    a[u][2 * i] = *reinterpret_cast<const float4*>(src + 32 * i);
+                    a[u][2 * i + 1] = *reinterpret_cast<const float4*>(src + 32 * i + 4);
+                }
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < SP; ++u) {
+            const float w = ms[u] == -INFINITY ? 0.f : fast_exp2(ms[u] - m0);
+            l = __builtin_fmaf(w, ls[u], l);
+#pragma unroll
+            for (int i = 0; i < NCH; ++i) {
+                const float4 a0 = a[u][2 * i], a1 = a[u][2 * i + 1];
+                float* c = acc + 8 * i;
+                c[0] = __builtin_fmaf(w, a0.x, c[0]);
+                c[1] = __builtin_fmaf(w, a0.y, c[1]);
+                c[2] = __builtin_fmaf(w, a0.z, c[2]);
+                c[3] = __builtin_fmaf(w, a0.w, c[3]);
+                c[4] = __builtin_fmaf(w, a1.x, c[4]);
+                c[5] = __builtin_fmaf(w, a1.y, c[5]);
+                c[6] = __builtin_fmaf(w, a1.z, c[6]);
+                c[7] = __builtin_fmaf(w, a1.w, c[7]);
+            }
         }
     }
 }
