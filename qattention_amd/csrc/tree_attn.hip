@@ -69,13 +69,21 @@ __global__ __launch_bounds__(kThreads) void tree_gather_kernel(TreeParams p) {
     Vec16 qf[NCH];
     load_q4<D>(p, qrow, h, j, qf);
     float m = -INFINITY, l = 0.f, acc[8 * NCH];
+    // the first chunk of the walk's K/V loads is in flight while the prefix
+    // splits are merged (the walk does not depend on them)
+    Walk4<T, D, WALK, LAYOUT> w(p, seq, start, n, tok, h / p.group, j);
+    w.issue();
     if constexpr (PSTATE) {
         load_partial_state4<D>(p, qrow, h, j, m, l, acc);
     } else {
 #pragma unroll
         for (int e = 0; e < 8 * NCH; ++e) acc[e] = 0.f;
     }
-    gather_walk4<T, D, WALK, LAYOUT>(p, seq, start, n, tok, h / p.group, qf, j, m, l, acc);
+    w.fold(qf, m, l, acc);
+    while (w.more()) {
+        w.issue();
+        w.fold(qf, m, l, acc);
+    }
     write_out4<T, D, LSE>(p, qrow, h, j, m, l, acc);
 }
 

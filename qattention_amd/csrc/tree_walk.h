@@ -160,20 +160,34 @@ __device__ __forceinline__ void fold_scores(const float* s, const Vec16 (*vf)[NC
 // The ancestor walk of one query with K/V rows gathered from global memory:
 // steps s = 0..max_depth attend c_s iff c_s != c_{s-1} (src/ragged_attn.py:
 // 338-377 heap, :657-698 parents).  The loads of CH steps are issued together
-// before their scores are formed; the chunk loop stops once every lane's walk
-// has stalled (root reached or self-loop).
+// (issue) before their scores are formed and folded into the state (fold);
+// the walk stops once every lane's walk has stalled (root reached or
+// self-loop).  A caller may issue the first chunk before it builds the
+// initial state, so those loads overlap its own.
 template <typename T, int D, int WALK, int LAYOUT>
-__device__ __forceinline__ void gather_walk4(const TreeParams& p, int seq, int32_t start, int32_t n, int tok,
-                                             int kvh, const Vec16* qf, int j, float& m, float& l, float* acc) {
-    constexpr int NCH = D / 32;
-    constexpr int CH = 8 / NCH;  // 2 steps for D=128: 64 VGPRs of K/V loads in flight per lane
-    const int64_t kvb = kv_base(p, seq, start);
-    const uint16_t* kb = (const uint16_t*)p.k + (int64_t)kvh * p.sk_h + 8 * j;
-    const uint16_t* vb = (const uint16_t*)p.v + (int64_t)kvh * p.sv_h + 8 * j;
-    int32_t cur = tok, prev = -1;
-    for (int s0 = 0; s0 <= p.max_depth; s0 += CH) {
+struct Walk4 {
+    static constexpr int NCH = D / 32;
+    static constexpr int CH = 8 / NCH;  // 2 steps for D=128: 64 VGPRs of K/V loads in flight per lane
+    const TreeParams& p;
+    const int seq;
+    const int32_t start, n;
+    const int64_t kvb;
+    const uint16_t* kb;
+    const uint16_t* vb;
+    int32_t cur, prev;
+    int s0;
+    bool val[CH];
+    Vec16 kf[CH][NCH], vf[CH][NCH];
+
+    __device__ __forceinline__ Walk4(const TreeParams& p_, int seq_, int32_t start_, int32_t n_, int tok, int kvh,
+                                     int j)
+        : p(p_), seq(seq_), start(start_), n(n_), kvb(kv_base(p_, seq_, start_)),
+          kb((const uint16_t*)p_.k + (int64_t)kvh * p_.sk_h + 8 * j),
+          vb((const uint16_t*)p_.v + (int64_t)kvh * p_.sv_h + 8 * j), cur(tok), prev(-1), s0(0) {}
+
+    // Issue the K/V loads of steps s0 .. s0 + CH - 1.
+    __device__ __forceinline__ void issue() {
         int64_t ko[CH], vo[CH];
-        bool val[CH];
 #pragma unroll
         for (int t = 0; t < CH; ++t) {
             bool ok = (s0 + t <= p.max_depth) && (cur != prev);
@@ -193,7 +207,6 @@ __device__ __forceinline__ void gather_walk4(const TreeParams& p, int seq, int32
             prev = cur;
             cur = walk_next<WALK>(p, start, n, cur);
         }
-        Vec16 kf[CH][NCH], vf[CH][NCH];
 #pragma unroll
         for (int t = 0; t < CH; ++t) {
 #pragma unroll
@@ -206,6 +219,10 @@ __device__ __forceinline__ void gather_walk4(const TreeParams& p, int seq, int32
                 }
             }
         }
+    }
+
+    // Fold the issued chunk into (m, l, acc) and move to the next chunk.
+    __device__ __forceinline__ void fold(const Vec16* qf, float& m, float& l, float* acc) {
         float s[CH];
 #pragma unroll
         for (int t = 0; t < CH; ++t) {
@@ -213,8 +230,20 @@ __device__ __forceinline__ void gather_walk4(const TreeParams& p, int seq, int32
             s[t] = val[t] ? d : -INFINITY;
         }
         fold_scores<T, NCH, CH>(s, vf, m, l, acc);
-        if (!__any(cur != prev)) break;
+        s0 += CH;
     }
+
+    __device__ __forceinline__ bool more() const { return s0 <= p.max_depth && __any(cur != prev); }
+};
+
+template <typename T, int D, int WALK, int LAYOUT>
+__device__ __forceinline__ void gather_walk4(const TreeParams& p, int seq, int32_t start, int32_t n, int tok,
+                                             int kvh, const Vec16* qf, int j, float& m, float& l, float* acc) {
+    Walk4<T, D, WALK, LAYOUT> w(p, seq, start, n, tok, kvh, j);
+    do {
+        w.issue();
+        w.fold(qf, m, l, acc);
+    } while (w.more());
 }
 
 // Normalise and store one query's output (+ LSE from lane 0 of the group).
