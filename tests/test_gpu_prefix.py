@@ -244,3 +244,41 @@ def test_cfg5_sampled():
         ref = sdpa.padded_sdpa([Q[rows, heads]], [K[rows, heads]], [V[rows, heads]], [m],
                                [Kp[s, :, heads]], [Vp[s, :, heads]])[0][0]
         check_fp16(O[rows, heads].double().numpy(), ref.double().numpy(), f"cfg5 seq {s}")
+
+
+@pytest.mark.parametrize("num_splits", [0, 1])
+def test_prefix_graph_capture_replay(num_splits):
+    """ragged_attention_prefix records into a HIP graph (device cu_seqlens,
+    max_seqlen given, workspace from the caching allocator) and every replay
+    reproduces the eager O and LSE, with eager work between replays.  Split
+    count 0 picks several splits (prefix kernel + merge/walk kernel), 1 forces
+    the single-split path with the walk fused into the prefix kernel."""
+    ra = _ra()
+    B, b, d, Hq, Hkv, D, L = 2, 4, 3, 8, 2, 128, 1500
+    N = num_tree_nodes(b, d)
+    say("prefix graph", num_splits)
+    Q, K, V, cu = make_inputs([N] * B, Hq, D, 4242 + num_splits, Hkv=Hkv)
+    Kp, Vp = _prefix(B, L, Hkv, D, 4243)
+    args = (Q.to(DEV), K.to(DEV), V.to(DEV), cu.to(DEV), Kp.to(DEV), Vp.to(DEV), b, d)
+    kw = dict(max_seqlen=N, return_lse=True, num_splits=num_splits)
+    o_eager, lse_eager = ra.ragged_attention_prefix(*args, **kw)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        ra.ragged_attention_prefix(*args, **kw)
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        o, lse = ra.ragged_attention_prefix(*args, **kw)
+    for i in range(4):
+        o.zero_()
+        lse.zero_()
+        junk = torch.randn(1000, device=DEV).sum()  # eager work between replays
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(o, o_eager), f"replay {i}: O"
+        assert torch.equal(lse, lse_eager), f"replay {i}: LSE"
+        del junk
+    o_ref, lse_ref, _ = oracle_tree(Q, K, V, cu, b, d, Kp=Kp, Vp=Vp)
+    check_fp16(o_eager.double().cpu().numpy(), o_ref, "prefix graph")
+    assert np.abs(lse_eager.double().cpu().numpy() - lse_ref).max() <= 1e-4
