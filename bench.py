@@ -1,6 +1,6 @@
 """Benchmark of the tree-verify attention hot path on one MI355X.
 
-    python bench.py [--steps K] [--warmup W] [--config cfg2|cfg3|cfg4|cfg5] [--algo auto|gather|subtree]
+    python bench.py [--steps K] [--warmup W] [--config cfg2|cfg3|cfg4|cfg5|gen1024] [--algo auto|gather|subtree]
 
 A step is one full verify-attention call (all sequences, all heads, and the
 prefix KV cache when the config has one) over one batch of synthetic input,
@@ -41,12 +41,17 @@ PEAK_MFMA = 2.5e15    # FLOP/s, MI355X dense fp16 MFMA (vendor figure)
 CALLS_PER_GRAPH = 8
 SETTLE_S = 0.1        # untimed replays before the warmup steps (clock settling)
 
-# BASELINE.json configs[1..4]
+# BASELINE.json configs[1..4], and the explicit-parents workload of the
+# reference's model-generality benchmark (scripts/benchmark_model_generality.py:
+# 19-53: B=1, heap parents (i-1)//b with the root its own parent, b=10 d=7
+# capped at N=1024 nodes, Llama-3.1-8B heads; BASELINE.md quotes 113.0 µs on
+# unrecorded hardware)
 CONFIGS = {
     "cfg2": dict(B=4, b=4, d=5, H=32, Hkv=32, D=128, L=0, sigma=1.0),
     "cfg3": dict(B=8, b=2, d=9, H=32, Hkv=32, D=128, L=0, sigma=1.0),
     "cfg4": dict(B=4, b=4, d=3, H=32, Hkv=8, D=128, L=10240, sigma=1.0),
     "cfg5": dict(B=16, b=8, d=4, H=32, Hkv=32, D=128, L=2048, sigma=0.5),
+    "gen1024": dict(B=1, b=10, d=7, H=32, Hkv=32, D=128, L=0, sigma=1.0, N=1024, walk="parents"),
 }
 
 
@@ -54,10 +59,20 @@ def num_tree_nodes(b, d):
     return d + 1 if b == 1 else (b ** (d + 1) - 1) // (b - 1)
 
 
+def tree_size(c):
+    """Nodes per sequence: the complete tree, or the config's cap."""
+    return c.get("N", num_tree_nodes(c["b"], c["d"]))
+
+
+def heap_parents(b, n):
+    """Sequence-local parent array of a heap-indexed tree, the root its own parent."""
+    return [0] + [(i - 1) // b for i in range(1, n)]
+
+
 def make_set(c, seed, dtype):
     """Q, tree K, tree V (packed) and prefix K/V [B, L, Hkv, D], drawn in that order."""
     import torch
-    N = num_tree_nodes(c["b"], c["d"])
+    N = tree_size(c)
     T = c["B"] * N
     g = torch.Generator().manual_seed(seed)
     s = c["sigma"]
@@ -74,11 +89,15 @@ def make_set(c, seed, dtype):
 def model_costs(c):
     """Algorithmic HBM bytes and FLOPs of one call."""
     B, b, d, H, Hkv, D, L = (c[k] for k in ("B", "b", "d", "H", "Hkv", "D", "L"))
-    N = num_tree_nodes(b, d)
+    N = tree_size(c)
     T = B * N
     tree_bytes = 2 * T * D * (2 * H + 2 * Hkv)          # Q + O at H, tree K + V at Hkv
     prefix_bytes = 2 * 2 * B * L * Hkv * D                 # prefix K + V at Hkv
-    steps = sum((b ** k) * (k + 1) for k in range(d + 1)) if b > 1 else sum(k + 1 for k in range(d + 1))
+    # attended (query, key) pairs per sequence: min(depth, d) + 1 per node
+    depth = [0] * N
+    for i in range(1, N):
+        depth[i] = depth[(i - 1) // b] + 1 if b > 1 else i
+    steps = sum(min(x, d) + 1 for x in depth)
     tree_flops = 4 * D * H * B * steps
     prefix_flops = 4 * B * N * H * L * D
     return tree_bytes + prefix_bytes, tree_flops + prefix_flops, prefix_flops
@@ -123,7 +142,7 @@ def cpu_baseline(c, budget_s=20.0):
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
     B, b, d = c["B"], c["b"], c["d"]
-    N = num_tree_nodes(b, d)
+    N = tree_size(c)
     Q, K, V, Kp, Vp = make_set(c, B * 10000 + b * 100 + d, torch.float16)
     nseq = B
     if c["L"] and B * N * (N + c["L"]) * c["H"] > 4e9:
@@ -194,8 +213,9 @@ def main():
 
     c = CONFIGS[args.config]
     B, b, d, H, Hkv, D, L = (c[k] for k in ("B", "b", "d", "H", "Hkv", "D", "L"))
-    N = num_tree_nodes(b, d)
+    N = tree_size(c)
     T = B * N
+    parents_walk = c.get("walk") == "parents"
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     algo = {"auto": _lib.ALGO_AUTO, "gather": _lib.ALGO_GATHER, "subtree": _lib.ALGO_SUBTREE}[args.algo]
@@ -207,12 +227,15 @@ def main():
     for i in range(nsets):
         sets.append([t.to(dev) if t is not None else None for t in make_set(c, seed + i, torch.float16)])
     cu = torch.arange(0, (B + 1) * N, N, dtype=torch.int32, device=dev)
+    parents = torch.tensor(heap_parents(b, N) * B, dtype=torch.int32, device=dev) if parents_walk else None
     torch.cuda.synchronize()
 
     def call(i):
         Q, K, V, Kp, Vp = sets[i]
         if L:
             return ra.ragged_attention_prefix(Q, K, V, cu, Kp, Vp, b, d, max_seqlen=N)
+        if parents_walk:
+            return ra.ragged_attention_with_parents(Q, K, V, cu, parents, d, max_seqlen=N)[0]
         return ra._tree_forward(Q, K, V, cu, b, d, N, False, algo)[0]
 
     for i in range(nsets):
@@ -297,7 +320,7 @@ def main():
         "dtype": "f16",
         "data": f"synthetic N(0,{c['sigma']}^2), CPU-seeded (seed B*10000+b*100+d), {nsets} rotating sets",
         "config": {"workload": f"{args.config}: verify attention B={B} b={b} d={d} N={N} H={H} Hkv={Hkv} "
-                               f"D={D} L={L} fp16", "B": B, "b": b, "d": d, "N": N, "H": H, "Hkv": Hkv,
+                               f"D={D} L={L} fp16" + (", explicit parents" if parents_walk else ""), "B": B, "b": b, "d": d, "N": N, "H": H, "Hkv": Hkv,
                    "D": D, "L": L, "tokens": T, "algo": args.algo},
         "achieved_GBps": round(achieved_bw / 1e9, 1),
         "wall_us_per_call": round(wall_us, 2),
