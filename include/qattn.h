@@ -161,7 +161,10 @@ int qattn_ancestors(const int32_t *cu_seqlens, const int32_t *parents, int32_t b
  * Prefix key/value row j of sequence s, kv head g, is
  *   k_prefix + s*kp_stride[0] + j*kp_stride[1] + g*kp_stride[2]
  * (kp_stride[0] == 0 shares one prefix across the batch; K/V heads are GQA
- * heads, never repeated).  Tree key/value row of local ancestor x of sequence
+ * heads, never repeated).  Prefix strides are multiples of 8 elements with
+ * 16-byte aligned pointers, and the token strides kp_stride[1], vp_stride[1]
+ * are non-negative and below 2^25 elements (else QATTN_ERR_LAYOUT): the
+ * kernel addresses a 64-key block with 32-bit byte offsets.  Tree key/value row of local ancestor x of sequence
  * s is  tree_seq_stride ? s*tree_seq_stride + tree_row0 + x : cu_seqlens[s] + x
  * (the reference hybrid layout [B*(L+N), H, D] is tree_seq_stride = L+N,
  * tree_row0 = L).  The prefix is computed with v_mfma_f32_16x16x32 in splits
