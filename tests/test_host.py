@@ -110,6 +110,25 @@ def test_abi_validation_other_entry_points():
     assert L.qattn_lse_merge(FAKE, s3, FAKE, s3, FAKE, ok4, FAKE, ok4, FAKE, ok4, 1, 4, 15, 64, 3, None) == -2
 
 
+def test_abi_prefix_stride_limits():
+    """The prefix kernel addresses a 64-key block with 32-bit byte offsets:
+    token strides of 2^25 elements or more, or negative ones, are a layout
+    error; an in-range layout gets past that check (and stops at the missing
+    workspace, before any launch)."""
+    L = _lib.lib()
+    ok3 = _lib.i64arr((256, 64, 1))
+
+    def call(kp):
+        return L.qattn_prefix_tree_fwd(FAKE, ok3, FAKE, ok3, FAKE, ok3, FAKE, _lib.i64arr(kp), FAKE,
+                                       _lib.i64arr((512 * 256, 256, 64)), 512, FAKE, ok3, None, None, FAKE,
+                                       1, 15, 15, 0, 0, 4, 4, 64, 2, 3, 0.125, 0, None, 0, 0, None)
+
+    assert call((1 << 40, 1 << 25, 64)) == -4
+    assert call((512 * 256, -256, 64)) == -4
+    assert call((512 * 256, (1 << 25) - 8, 64)) == -5
+    assert call((512 * 256, 256, 64)) == -5
+
+
 # ---------------------------------------------------------------------------
 # Python API behaviour on the host
 # ---------------------------------------------------------------------------
