@@ -23,6 +23,7 @@
 //    state to the ancestor walk in the same workgroup (gather_walk4), which
 //    normalises and stores O -- no partial state leaves the chip.
 #include <algorithm>
+#include <type_traits>
 
 #include "qattn_common.h"
 #include "qattn_device.h"
@@ -415,54 +416,81 @@ __global__ __launch_bounds__(kPrefixThreads) __attribute__((amdgpu_waves_per_eu(
                     make_float4(oacc[b][dt][0], oacc[b][dt][1], oacc[b][dt][2], oacc[b][dt][3]);
         }
     } else {
-        // ---- fused epilogue: re-lay each 16-row block in LDS as 4 lanes per
-        // query and run the ancestor walk from this state ----
-        constexpr int OROW = D + 4;  // fp32 row stride (pad)
-        // each wave stages its 16-row blocks in one of the four K/V buffers
-        uint16_t* wbuf = wave == 0 ? Kb0 : (wave == 1 ? Kb1 : (wave == 2 ? Vb0 : Vb1));
-        float* Os = reinterpret_cast<float*>(wbuf);
-        float* Ms = Os + 16 * OROW;
-        static_assert((16 * OROW + 32) * 4 <= BLK * 2, "epilogue staging must fit one K/V buffer");
-        const int grp = lane >> 2, j = lane & 3;
+        // ---- fused epilogue: each wave re-lays both of its 16-row blocks in
+        // its own LDS buffer as 4 lanes per query (no other wave reads it, so
+        // only the wave's own LDS order matters), takes m and l by shuffles,
+        // and runs the two ancestor walks with their loads interleaved ----
+        static_assert(kQB == 2, "the epilogue walks two column blocks together");
         constexpr int NCH = D / 32;
+        constexpr int C4 = D / 4;  // float4 per staged row; float4 c of row r sits at c ^ (r & 7)
+        uint16_t* wbuf = wave == 0 ? Kb0 : (wave == 1 ? Kb1 : (wave == 2 ? Vb0 : Vb1));
+        float4* Os = reinterpret_cast<float4*>(wbuf);  // [kQB * 16 rows][C4]
+        static_assert(kQB * 16 * D * 4 <= BLK * 2, "epilogue staging must fit one K/V buffer");
 #pragma unroll
         for (int b = 0; b < kQB; ++b) {
+            const int row = 16 * b + l16;
 #pragma unroll
             for (int dt = 0; dt < ND; ++dt)
-                *reinterpret_cast<float4*>(Os + l16 * OROW + 16 * dt + 4 * lq) =
+                Os[row * C4 + ((4 * dt + lq) ^ (row & 7))] =
                     make_float4(oacc[b][dt][0], oacc[b][dt][1], oacc[b][dt][2], oacc[b][dt][3]);
-            if (lq == 0) {
-                Ms[l16] = m_run[b];
-                Ms[16 + l16] = l_tot[b];
-            }
-            __syncthreads();
-            const int rr = qt * kBM + wave * (16 * kQB) + 16 * b + grp;
-            if (rr < rows) {
-                const int tok = divide(rr, p.gdiv);
-                const int h = kvh * g + (rr - tok * g);
-                const int64_t qr = (int64_t)s0 + tok;
-                float acc[8 * NCH];
-#pragma unroll
-                for (int i = 0; i < NCH; ++i) {
-                    const float4 a0 = *reinterpret_cast<const float4*>(Os + grp * OROW + 8 * (j + 4 * i));
-                    const float4 a1 = *reinterpret_cast<const float4*>(Os + grp * OROW + 8 * (j + 4 * i) + 4);
-                    acc[8 * i + 0] = a0.x;
-                    acc[8 * i + 1] = a0.y;
-                    acc[8 * i + 2] = a0.z;
-                    acc[8 * i + 3] = a0.w;
-                    acc[8 * i + 4] = a1.x;
-                    acc[8 * i + 5] = a1.y;
-                    acc[8 * i + 6] = a1.z;
-                    acc[8 * i + 7] = a1.w;
-                }
-                float m = Ms[grp], l = Ms[16 + grp];
-                Vec16 qf4[NCH];
-                load_q4<D>(tp, qr, h, j, qf4);
-                gather_walk4<T, D, WALK_HEAP, KV_PACKED>(tp, seq, s0, n, tok, kvh, qf4, j, m, l, acc);
-                write_out4<T, D, LSE>(tp, qr, h, j, m, l, acc);
-            }
-            __syncthreads();
         }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        const int grp = lane >> 2, j = lane & 3;
+        float acc[kQB][8 * NCH], mw[kQB], lw[kQB];
+        int tokb[kQB], hb[kQB];
+        int64_t qrb[kQB];
+        bool vb[kQB];
+        Vec16 qf4[kQB][NCH];
+#pragma unroll
+        for (int b = 0; b < kQB; ++b) {
+            const int rr = qt * kBM + wave * (16 * kQB) + 16 * b + grp;
+            vb[b] = rr < rows;
+            // a row past the tile's queries walks token 0 (valid memory) and stores nothing
+            tokb[b] = vb[b] ? divide(rr, p.gdiv) : 0;
+            hb[b] = kvh * g + (vb[b] ? rr - tokb[b] * g : 0);
+            qrb[b] = (int64_t)s0 + tokb[b];
+            const int row = 16 * b + grp;
+#pragma unroll
+            for (int i = 0; i < NCH; ++i) {
+                const float4 a0 = Os[row * C4 + ((2 * (j + 4 * i)) ^ (row & 7))];
+                const float4 a1 = Os[row * C4 + ((2 * (j + 4 * i) + 1) ^ (row & 7))];
+                acc[b][8 * i + 0] = a0.x;
+                acc[b][8 * i + 1] = a0.y;
+                acc[b][8 * i + 2] = a0.z;
+                acc[b][8 * i + 3] = a0.w;
+                acc[b][8 * i + 4] = a1.x;
+                acc[b][8 * i + 5] = a1.y;
+                acc[b][8 * i + 6] = a1.z;
+                acc[b][8 * i + 7] = a1.w;
+            }
+            // query grp's state is held by lane grp of the MFMA layout (l16 = grp, lq = 0)
+            mw[b] = __shfl(m_run[b], grp);
+            lw[b] = __shfl(l_tot[b], grp);
+            load_q4<D>(tp, qrb[b], hb[b], j, qf4[b]);
+        }
+        // steps per chunk of each walk: half the single-walk chunk where two
+        // full chunks in flight spilled registers (bf16 at D=128, D=64)
+        constexpr int CH1 = 8 / NCH;
+        constexpr int CHW = (D == 64 || (D == 128 && std::is_same<T, BF16>::value)) ? CH1 / 2 : CH1;
+        using W = Walk4<T, D, WALK_HEAP, KV_PACKED, CHW>;
+        W w0(tp, seq, s0, n, tokb[0], kvh, j), w1(tp, seq, s0, n, tokb[1], kvh, j);
+        w0.issue();
+        w1.issue();
+        w0.fold(qf4[0], mw[0], lw[0], acc[0]);
+        w1.fold(qf4[1], mw[1], lw[1], acc[1]);
+        for (;;) {
+            const bool a0 = w0.more(), a1 = w1.more();
+            if (!a0 && !a1) break;
+            if (a0) w0.issue();
+            if (a1) w1.issue();
+            if (a0) w0.fold(qf4[0], mw[0], lw[0], acc[0]);
+            if (a1) w1.fold(qf4[1], mw[1], lw[1], acc[1]);
+        }
+#pragma unroll
+        for (int b = 0; b < kQB; ++b)
+            if (vb[b]) write_out4<T, D, LSE>(tp, qrb[b], hb[b], j, mw[b], lw[b], acc[b]);
     }
 }
 

@@ -164,10 +164,10 @@ __device__ __forceinline__ void fold_scores(const float* s, const Vec16 (*vf)[NC
 // the walk stops once every lane's walk has stalled (root reached or
 // self-loop).  A caller may issue the first chunk before it builds the
 // initial state, so those loads overlap its own.
-template <typename T, int D, int WALK, int LAYOUT>
+template <typename T, int D, int WALK, int LAYOUT, int CH_ = 8 / (D / 32)>
 struct Walk4 {
     static constexpr int NCH = D / 32;
-    static constexpr int CH = 8 / NCH;  // 2 steps for D=128: 64 VGPRs of K/V loads in flight per lane
+    static constexpr int CH = CH_;  // default 2 steps at D=128: 64 VGPRs of K/V loads in flight per lane
     const TreeParams& p;
     const int seq;
     const int32_t start, n;
