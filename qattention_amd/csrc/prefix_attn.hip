@@ -23,7 +23,6 @@
 //    state to the ancestor walk in the same workgroup (gather_walk4), which
 //    normalises and stores O -- no partial state leaves the chip.
 #include <algorithm>
-#include <type_traits>
 
 #include "qattn_common.h"
 #include "qattn_device.h"
@@ -447,8 +446,9 @@ __global__ __launch_bounds__(kPrefixThreads) __attribute__((amdgpu_waves_per_eu(
         for (int b = 0; b < kQB; ++b) {
             const int rr = qt * kBM + wave * (16 * kQB) + 16 * b + grp;
             vb[b] = rr < rows;
-            // a row past the tile's queries walks token 0 (valid memory) and stores nothing
-            tokb[b] = vb[b] ? divide(rr, p.gdiv) : 0;
+            // a row past the tile's queries walks the tile's first token (valid
+            // memory, ancestors inside the staged ranges) and stores nothing
+            tokb[b] = vb[b] ? divide(rr, p.gdiv) : (qt * kBM) / g;
             hb[b] = kvh * g + (vb[b] ? rr - tokb[b] * g : 0);
             qrb[b] = (int64_t)s0 + tokb[b];
             const int row = 16 * b + grp;
@@ -470,23 +470,108 @@ __global__ __launch_bounds__(kPrefixThreads) __attribute__((amdgpu_waves_per_eu(
             lw[b] = __shfl(l_tot[b], grp);
             load_q4<D>(tp, qrb[b], hb[b], j, qf4[b]);
         }
-        // steps per chunk of each walk: half the single-walk chunk where two
-        // full chunks in flight spilled registers (bf16 at D=128, D=64)
-        constexpr int CH1 = 8 / NCH;
-        constexpr int CHW = (D == 64 || (D == 128 && std::is_same<T, BF16>::value)) ? CH1 / 2 : CH1;
-        using W = Walk4<T, D, WALK_HEAP, KV_PACKED, CHW>;
-        W w0(tp, seq, s0, n, tokb[0], kvh, j), w1(tp, seq, s0, n, tokb[1], kvh, j);
-        w0.issue();
-        w1.issue();
-        w0.fold(qf4[0], mw[0], lw[0], acc[0]);
-        w1.fold(qf4[1], mw[1], lw[1], acc[1]);
-        for (;;) {
-            const bool a0 = w0.more(), a1 = w1.more();
-            if (!a0 && !a1) break;
-            if (a0) w0.issue();
-            if (a1) w1.issue();
-            if (a0) w0.fold(qf4[0], mw[0], lw[0], acc[0]);
-            if (a1) w1.fold(qf4[1], mw[1], lw[1], acc[1]);
+        // Heap parents are monotonic, so walk step t of every token in the
+        // tile's range [tl, th] lies in [par^t(tl), par^t(th)].  When those
+        // ranges (steps 1 ..) total at most 128 rows they are staged once in
+        // LDS, level after level (K rows in Kb0/Kb1, V rows in Vb0/Vb1, 64 rows
+        // per buffer), and the walks read them there; each query's own row
+        // (step 0) comes from global memory.  Otherwise the walks gather every
+        // step from global memory.
+        constexpr int kRowsPerBuf = BLK / D;
+        constexpr int kLdsRows = 2 * kRowsPerBuf;
+        const int tl = (qt * kBM) / g;
+        const int th = (min(qt * kBM + kBM, rows) - 1) / g;
+        int nlev = 0, total = 0;
+        {
+            int lo = tl, hi = th;
+            for (int t = 1; t <= tp.max_depth && total <= kLdsRows; ++t) {
+                if (lo == 0 && hi == 0) break;  // past the root every step is a self-loop
+                lo = heap_parent(lo, tp.bdiv);
+                hi = heap_parent(hi, tp.bdiv);
+                total += hi - lo + 1;
+                nlev = t;
+            }
+        }
+        if (total <= kLdsRows) {
+            const int64_t kvb = kv_base(tp, seq, s0);
+            const uint16_t* kg = (const uint16_t*)tp.k + (int64_t)kvh * tp.sk_h;
+            const uint16_t* vg = (const uint16_t*)tp.v + (int64_t)kvh * tp.sv_h;
+            auto krow = [&](int slot) { return (slot < kRowsPerBuf ? Kb0 : Kb1) + (slot % kRowsPerBuf) * D; };
+            auto vrow = [&](int slot) { return (slot < kRowsPerBuf ? Vb0 : Vb1) + (slot % kRowsPerBuf) * D; };
+            // step 0 loads go out before the staging
+            Vec16 k0[kQB][NCH], v0[kQB][NCH];
+#pragma unroll
+            for (int b = 0; b < kQB; ++b)
+#pragma unroll
+                for (int i = 0; i < NCH; ++i) {
+                    k0[b][i] = ld16(kg + (kvb + tokb[b]) * tp.sk_t + 8 * j + 32 * i);
+                    v0[b][i] = ld16(vg + (kvb + tokb[b]) * tp.sv_t + 8 * j + 32 * i);
+                }
+            __syncthreads();  // every wave has read its staged O
+            {
+                int lo = tl, hi = th, off = 0;
+                for (int t = 1; t <= nlev; ++t) {
+                    lo = heap_parent(lo, tp.bdiv);
+                    hi = heap_parent(hi, tp.bdiv);
+                    const int sz = hi - lo + 1;
+                    for (int idx = tid; idx < sz * DV; idx += kPrefixThreads) {
+                        const int r = idx / DV, c = idx - r * DV;
+                        const int64_t grow = kvb + lo + r;
+                        st16(krow(off + r) + 8 * c, ld16(kg + grow * tp.sk_t + 8 * c));
+                        st16(vrow(off + r) + 8 * c, ld16(vg + grow * tp.sv_t + 8 * c));
+                    }
+                    off += sz;
+                }
+            }
+            __syncthreads();
+            int32_t cur[kQB], prev[kQB];
+#pragma unroll
+            for (int b = 0; b < kQB; ++b) {
+                float sc = qk4<T, NCH>(qf4[b], k0[b]) * tp.scale_log2;
+                fold_scores<T, NCH, 1>(&sc, &v0[b], mw[b], lw[b], acc[b]);
+                prev[b] = tokb[b];
+                cur[b] = heap_parent(tokb[b], tp.bdiv);
+            }
+            int lo = tl, hi = th, off = 0;
+            for (int t = 1; t <= nlev; ++t) {
+                lo = heap_parent(lo, tp.bdiv);
+                hi = heap_parent(hi, tp.bdiv);
+#pragma unroll
+                for (int b = 0; b < kQB; ++b) {
+                    const int slot = off + cur[b] - lo;  // inside [off, off + hi - lo] by monotonicity
+                    Vec16 kk[NCH], vv[1][NCH];
+#pragma unroll
+                    for (int i = 0; i < NCH; ++i) {
+                        kk[i] = ld16(krow(slot) + 8 * j + 32 * i);
+                        vv[0][i] = ld16(vrow(slot) + 8 * j + 32 * i);
+                    }
+                    float sc = qk4<T, NCH>(qf4[b], kk) * tp.scale_log2;
+                    sc = cur[b] != prev[b] ? sc : -INFINITY;  // the root's self-loop is not a step
+                    fold_scores<T, NCH, 1>(&sc, vv, mw[b], lw[b], acc[b]);
+                    prev[b] = cur[b];
+                    cur[b] = heap_parent(cur[b], tp.bdiv);
+                }
+                off += hi - lo + 1;
+            }
+        } else {
+            // steps per chunk of each walk: half the single-walk chunk from
+            // D = 64 up (two full chunks in flight spill registers there)
+            constexpr int CH1 = 8 / NCH;
+            constexpr int CHW = D >= 64 ? CH1 / 2 : CH1;
+            using W = Walk4<T, D, WALK_HEAP, KV_PACKED, CHW>;
+            W w0(tp, seq, s0, n, tokb[0], kvh, j), w1(tp, seq, s0, n, tokb[1], kvh, j);
+            w0.issue();
+            w1.issue();
+            w0.fold(qf4[0], mw[0], lw[0], acc[0]);
+            w1.fold(qf4[1], mw[1], lw[1], acc[1]);
+            for (;;) {
+                const bool a0 = w0.more(), a1 = w1.more();
+                if (!a0 && !a1) break;
+                if (a0) w0.issue();
+                if (a1) w1.issue();
+                if (a0) w0.fold(qf4[0], mw[0], lw[0], acc[0]);
+                if (a1) w1.fold(qf4[1], mw[1], lw[1], acc[1]);
+            }
         }
 #pragma unroll
         for (int b = 0; b < kQB; ++b)

@@ -282,3 +282,23 @@ def test_prefix_graph_capture_replay(num_splits):
     o_ref, lse_ref, _ = oracle_tree(Q, K, V, cu, b, d, Kp=Kp, Vp=Vp)
     check_fp16(o_eager.double().cpu().numpy(), o_ref, "prefix graph")
     assert np.abs(lse_eager.double().cpu().numpy() - lse_ref).max() <= 1e-4
+
+
+@pytest.mark.parametrize("b,d,D,Hq,Hkv", [(2, 9, 128, 4, 4), (2, 8, 64, 8, 2), (3, 6, 128, 2, 2), (8, 3, 128, 4, 4)])
+def test_prefix_fused_walk_paths(b, d, D, Hq, Hkv):
+    """One prefix split runs the ancestor walk inside the prefix kernel: a
+    tile whose ancestor ranges fit 128 rows walks them from LDS, others gather
+    from global memory.  Deep binary trees (128-token tiles near the leaves
+    need ~140 ancestor rows) exercise both in one call, wider trees the LDS
+    path only."""
+    ra = _ra()
+    N = num_tree_nodes(b, d)
+    L = 200
+    say("fused walk", b, d, D, Hq, Hkv)
+    Q, K, V, cu = make_inputs([N, N // 2 + 1], Hq, D, 7000 + b * 10 + d, Hkv=Hkv)
+    Kp, Vp = _prefix(2, L, Hkv, D, 7001 + b * 10 + d)
+    O, LSE = ra.ragged_attention_prefix(Q.to(DEV), K.to(DEV), V.to(DEV), cu, Kp.to(DEV), Vp.to(DEV), b, d,
+                                        return_lse=True, num_splits=1)
+    o_ref, lse_ref, _ = oracle_tree(Q, K, V, cu, b, d, Kp=Kp, Vp=Vp)
+    check_fp16(O.double().cpu().numpy(), o_ref, "fused walk")
+    assert np.abs(LSE.double().cpu().numpy() - lse_ref).max() <= 1e-4
