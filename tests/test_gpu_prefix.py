@@ -302,3 +302,26 @@ def test_prefix_fused_walk_paths(b, d, D, Hq, Hkv):
     o_ref, lse_ref, _ = oracle_tree(Q, K, V, cu, b, d, Kp=Kp, Vp=Vp)
     check_fp16(O.double().cpu().numpy(), o_ref, "fused walk")
     assert np.abs(LSE.double().cpu().numpy() - lse_ref).max() <= 1e-4
+
+
+def test_prefix_empty_and_zero_length_sequences():
+    """A zero-length sequence between others leaves its (absent) rows alone
+    and does not disturb its neighbours, through both the split and the fused
+    path; an empty batch returns empty O and LSE."""
+    ra = _ra()
+    lens, Hq, Hkv, D, L, b, md = [13, 0, 40, 1], 4, 2, 128, 300, 3, 3
+    say("prefix zero-length", lens)
+    Q, K, V, cu = make_inputs(lens, Hq, D, 5150, Hkv=Hkv)
+    Kp, Vp = _prefix(len(lens), L, Hkv, D, 5151)
+    o_ref, lse_ref, _ = oracle_tree(Q, K, V, cu, b, md, Kp=Kp, Vp=Vp)
+    for ns in (0, 1):
+        O, LSE = ra.ragged_attention_prefix(Q.to(DEV), K.to(DEV), V.to(DEV), cu, Kp.to(DEV), Vp.to(DEV), b, md,
+                                            return_lse=True, num_splits=ns)
+        check_fp16(O.double().cpu().numpy(), o_ref, f"zero-length splits={ns}")
+        assert np.abs(LSE.double().cpu().numpy() - lse_ref).max() <= 1e-4
+    Qe = torch.zeros(0, Hq, D, dtype=torch.float16, device=DEV)
+    Ke = torch.zeros(0, Hkv, D, dtype=torch.float16, device=DEV)
+    cue = torch.zeros(1, dtype=torch.int32)
+    Kpe = torch.zeros(0, L, Hkv, D, dtype=torch.float16, device=DEV)
+    O, LSE = ra.ragged_attention_prefix(Qe, Ke, Ke, cue, Kpe, Kpe, b, md, return_lse=True)
+    assert O.shape == (0, Hq, D) and LSE.shape == (0, Hq)
