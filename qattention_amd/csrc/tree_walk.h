@@ -55,31 +55,22 @@ __device__ __forceinline__ void load_q4(const TreeParams& p, int64_t qrow, int h
 }
 
 // Initial state from split-K prefix partials (flash-decoding merge of all
-// splits): m = max_s m_s, l = sum_s 2^(m_s - m) l_s, acc likewise.  The loads
-// of several splits are issued together (8 maxima, then 16 float4 of partial
-// numerators per step), so a merge of n splits waits on about n / 8 + n / SP
-// memory round trips rather than 2 n.
+// splits): m = max_s m_s, l = sum_s 2^(m_s - m) l_s, acc likewise.  The splits
+// are folded in batches of SP whose loads are issued together, each batch
+// moving the running maximum once (an online merge: no separate pass for the
+// maxima), so n splits cost about n / SP memory round trips.
 template <int D>
 __device__ __forceinline__ void load_partial_state4(const TreeParams& p, int64_t qrow, int h, int j,
                                                     float& m, float& l, float* acc) {
     constexpr int NCH = D / 32;
-    constexpr int SP = 8 / NCH;  // splits per step of the weighted sum
+    constexpr int SP = 12 / NCH;  // splits per batch: 3 at head_dim 128
     const int ns = p.n_split;
     const int64_t plane = p.total_tokens * (int64_t)p.Hq;
     const int64_t idx = qrow * p.Hq + h;
-    float m0 = -INFINITY;
-    for (int s0 = 0; s0 < ns; s0 += 8) {
-        float v[8];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) v[u] = s0 + u < ns ? p.part_m[(s0 + u) * plane + idx] : -INFINITY;
-#pragma unroll
-        for (int u = 0; u < 8; ++u) m0 = fmaxf(m0, v[u]);
-    }
-    m = m0;
+    m = -INFINITY;
     l = 0.f;
 #pragma unroll
     for (int e = 0; e < 8 * NCH; ++e) acc[e] = 0.f;
-    if (m0 == -INFINITY) return;
     for (int s0 = 0; s0 < ns; s0 += SP) {
         float ms[SP], ls[SP];
         float4 a[SP][2 * NCH];
@@ -101,9 +92,20 @@ __device__ __forceinline__ void load_partial_state4(const TreeParams& p, int64_t
                 }
             }
         }
+        float mb = m;
+#pragma unroll
+        for (int u = 0; u < SP; ++u) mb = fmaxf(mb, ms[u]);
+        if (mb == -INFINITY) continue;  // nothing attended so far
+        if (m != -INFINITY && mb != m) {
+            const float alpha = fast_exp2(m - mb);
+            l *= alpha;
+#pragma unroll
+            for (int e = 0; e < 8 * NCH; ++e) acc[e] *= alpha;
+        }
+        m = mb;
 #pragma unroll
         for (int u = 0; u < SP; ++u) {
-            const float w = ms[u] == -INFINITY ? 0.f : fast_exp2(ms[u] - m0);
+            const float w = ms[u] == -INFINITY ? 0.f : fast_exp2(ms[u] - m);
             l = __builtin_fmaf(w, ls[u], l);
 #pragma unroll
             for (int i = 0; i < NCH; ++i) {
