@@ -459,6 +459,36 @@ def test_subtree_schedule_repeats():
     torch.cuda.synchronize()
 
 
+def test_subtree_concurrent_streams():
+    """Eager subtree launches in flight on four streams at once take
+    different counter slots of the per-device ring: every stream's results
+    are bit-identical to its inputs run alone (a slot shared by two running
+    launches would hand tiles of one to the other's workgroups)."""
+    ra, _ = _ra()
+    B, b, d, H = 4, 4, 5, 32
+    N = num_tree_nodes(b, d)
+    say("concurrent streams", B, b, d, H)
+    cu = torch.arange(0, (B + 1) * N, N, dtype=torch.int32, device=DEV)
+    sets, refs = [], []
+    for sidx in range(4):
+        Q, K, V, _ = make_inputs([N] * B, H, 128, 900 + sidx)
+        sets.append((Q.to(DEV), K.to(DEV), V.to(DEV)))
+        refs.append(ra._tree_forward(*sets[-1], cu, b, d, N, False, 2)[0].clone())
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream() for _ in range(4)]
+    for st in streams:
+        st.wait_stream(torch.cuda.current_stream())
+    outs = [[] for _ in range(4)]
+    for it in range(6):
+        for sidx, st in enumerate(streams):
+            with torch.cuda.stream(st):
+                outs[sidx].append(ra._tree_forward(*sets[sidx], cu, b, d, N, False, 2)[0])
+    torch.cuda.synchronize()
+    for sidx in range(4):
+        for it, o in enumerate(outs[sidx]):
+            assert torch.equal(o, refs[sidx]), f"stream {sidx} launch {it}"
+
+
 @pytest.mark.parametrize("B,b,d,H", [(4, 4, 4, 8), (4, 4, 5, 32)])
 def test_graph_capture_replay(B, b, d, H):
     """The entry point records into a HIP graph (device cu + max_seqlen) and
