@@ -36,7 +36,7 @@
  *     computed).  A sequence whose offsets are decreasing, negative or beyond
  *     total_tokens is skipped (its output rows are left untouched).
  *   - scale multiplies q.k (the reference fixes it to 1/sqrt(head_dim));
- *     qattn_prefix_tree_fwd requires scale > 0.
+ *     the prefix entry points require scale > 0.
  *   - lse (optional, may be NULL) is fp32 [tokens, num_q_heads] with strides
  *     {stride_token, stride_head}: lse = m + ln(sum exp(s - m)).
  */
@@ -192,6 +192,33 @@ int qattn_prefix_tree_fwd(const void *q, const int64_t q_stride[3],
                           int32_t branching_factor, int32_t max_depth, float scale,
                           int32_t dtype, void *workspace, int64_t workspace_size,
                           int32_t num_splits, void *stream);
+
+/*
+ * The same over an explicit parent array (EAGLE-3 dynamic trees) instead of a
+ * heap tree: parents as in qattn_tree_parents_fwd, everything else as in
+ * qattn_prefix_tree_fwd (same workspace size).
+ *
+ * Replaces the reference E2E verify composition for a tree with parents:
+ * prefix flash attention with LSE + ragged_attention_with_parents +
+ * fused_lse_merge (scripts/e2e_benchmark.py:1427-1496, the tree_parents
+ * branch at :1466-1474; kernels src/ragged_attn.py:588-714, 1575-1616), in
+ * one call, GQA-native, without the intermediate O/LSE tensors.
+ */
+int qattn_prefix_tree_parents_fwd(const void *q, const int64_t q_stride[3],
+                                  const void *k, const int64_t k_stride[3],
+                                  const void *v, const int64_t v_stride[3],
+                                  const void *k_prefix, const int64_t kp_stride[3],
+                                  const void *v_prefix, const int64_t vp_stride[3],
+                                  int32_t prefix_len,
+                                  void *o, const int64_t o_stride[3],
+                                  float *lse, const int64_t lse_stride[2],
+                                  const int32_t *cu_seqlens, const int32_t *parents,
+                                  int32_t batch, int32_t max_seqlen, int64_t total_tokens,
+                                  int64_t tree_seq_stride, int64_t tree_row0,
+                                  int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                                  int32_t max_depth, float scale, int32_t dtype,
+                                  void *workspace, int64_t workspace_size,
+                                  int32_t num_splits, void *stream);
 
 /*
  * Two-state softmax merge.

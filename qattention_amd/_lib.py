@@ -52,6 +52,10 @@ SIGNATURES = {
         _p, _i64p, _p, _i64p, _p, _i64p, _p, _i64p, _p, _i64p, _i32,
         _p, _i64p, _p, _i64p, _p, _i32, _i32, _i64, _i64, _i64,
         _i32, _i32, _i32, _i32, _i32, _f32, _i32, _p, _i64, _i32, _p]),
+    "qattn_prefix_tree_parents_fwd": (C.c_int, [
+        _p, _i64p, _p, _i64p, _p, _i64p, _p, _i64p, _p, _i64p, _i32,
+        _p, _i64p, _p, _i64p, _p, _p, _i32, _i32, _i64, _i64, _i64,
+        _i32, _i32, _i32, _i32, _f32, _i32, _p, _i64, _i32, _p]),
     "qattn_lse_merge": (C.c_int, [
         _p, _i64p, _p, _i64p, _p, _i64p, _p, _i64p, _p, _i64p,
         _i32, _i32, _i32, _i32, _i32, _p]),

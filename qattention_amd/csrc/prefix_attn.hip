@@ -66,7 +66,9 @@ __device__ __forceinline__ int kv_swz(int r, int dv) {
 // s_waitcnt immediate (gfx9 encoding): vmcnt N, expcnt and lgkmcnt unconstrained
 constexpr int kWaitVm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 
-template <typename T, int D, bool FUSED, bool LSE>
+// WALK: the tree walk of the fused epilogue (heap or explicit parents); the
+// split kernels leave the walk to the tree kernels.
+template <typename T, int D, bool FUSED, bool LSE, int WALK = WALK_HEAP>
 __global__ __launch_bounds__(kPrefixThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefix_attn_kernel(
     PrefixParams p, TreeParams tp) {
     constexpr int NC = D / 32;      // MFMA k-chunks over the head dim
@@ -477,12 +479,13 @@ __global__ __launch_bounds__(kPrefixThreads) __attribute__((amdgpu_waves_per_eu(
         // per buffer), and the walks read them there; each query's own row
         // (step 0) comes from global memory.  Otherwise the walks gather every
         // step from global memory.
+        // (The explicit-parents walk has no such ranges and always gathers.)
         constexpr int kRowsPerBuf = BLK / D;
         constexpr int kLdsRows = 2 * kRowsPerBuf;
         const int tl = (qt * kBM) / g;
         const int th = (min(qt * kBM + kBM, rows) - 1) / g;
-        int nlev = 0, total = 0;
-        {
+        int nlev = 0, total = WALK == WALK_HEAP ? 0 : kLdsRows + 1;
+        if constexpr (WALK == WALK_HEAP) {
             int lo = tl, hi = th;
             for (int t = 1; t <= tp.max_depth && total <= kLdsRows; ++t) {
                 if (lo == 0 && hi == 0) break;  // past the root every step is a self-loop
@@ -492,7 +495,7 @@ __global__ __launch_bounds__(kPrefixThreads) __attribute__((amdgpu_waves_per_eu(
                 nlev = t;
             }
         }
-        if (total <= kLdsRows) {
+        if (WALK == WALK_HEAP && total <= kLdsRows) {
             const int64_t kvb = kv_base(tp, seq, s0);
             const uint16_t* kg = (const uint16_t*)tp.k + (int64_t)kvh * tp.sk_h;
             const uint16_t* vg = (const uint16_t*)tp.v + (int64_t)kvh * tp.sv_h;
@@ -558,7 +561,7 @@ __global__ __launch_bounds__(kPrefixThreads) __attribute__((amdgpu_waves_per_eu(
             // D = 64 up (two full chunks in flight spill registers there)
             constexpr int CH1 = 8 / NCH;
             constexpr int CHW = D >= 64 ? CH1 / 2 : CH1;
-            using W = Walk4<T, D, WALK_HEAP, KV_PACKED, CHW>;
+            using W = Walk4<T, D, WALK, KV_PACKED, CHW>;
             W w0(tp, seq, s0, n, tokb[0], kvh, j), w1(tp, seq, s0, n, tokb[1], kvh, j);
             w0.issue();
             w1.issue();
@@ -607,21 +610,23 @@ static int64_t workspace_bytes(int64_t total_tokens, int hq, int head_dim, int s
 }
 
 template <typename T, int D>
-static int launch_prefix(const PrefixParams& pp, const TreeParams& tp, bool fused, hipStream_t st) {
+static int launch_prefix(const PrefixParams& pp, const TreeParams& tp, bool fused, int walk, hipStream_t st) {
     const int64_t grid = ((int64_t)pp.n_units + 7) / 8 * 8;
     if (grid >= (int64_t(1) << 31)) {
         set_error("prefix grid too large");
         return QATTN_ERR_ARG;
     }
+    const dim3 g((unsigned)grid), b(kPrefixThreads);
     if (!fused)
-        hipLaunchKernelGGL((prefix_attn_kernel<T, D, false, false>), dim3((unsigned)grid), dim3(kPrefixThreads), 0,
-                           st, pp, tp);
+        hipLaunchKernelGGL((prefix_attn_kernel<T, D, false, false>), g, b, 0, st, pp, tp);
+    else if (walk == WALK_PARENTS && tp.lse)
+        hipLaunchKernelGGL((prefix_attn_kernel<T, D, true, true, WALK_PARENTS>), g, b, 0, st, pp, tp);
+    else if (walk == WALK_PARENTS)
+        hipLaunchKernelGGL((prefix_attn_kernel<T, D, true, false, WALK_PARENTS>), g, b, 0, st, pp, tp);
     else if (tp.lse)
-        hipLaunchKernelGGL((prefix_attn_kernel<T, D, true, true>), dim3((unsigned)grid), dim3(kPrefixThreads), 0,
-                           st, pp, tp);
+        hipLaunchKernelGGL((prefix_attn_kernel<T, D, true, true>), g, b, 0, st, pp, tp);
     else
-        hipLaunchKernelGGL((prefix_attn_kernel<T, D, true, false>), dim3((unsigned)grid), dim3(kPrefixThreads), 0,
-                           st, pp, tp);
+        hipLaunchKernelGGL((prefix_attn_kernel<T, D, true, false>), g, b, 0, st, pp, tp);
     return launch_status("prefix_attn_kernel");
 }
 
@@ -629,30 +634,17 @@ static int launch_prefix(const PrefixParams& pp, const TreeParams& tp, bool fuse
 
 using namespace qattn;
 
-extern "C" {
-
-int64_t qattn_prefix_workspace_bytes(int32_t batch, int32_t max_seqlen, int64_t total_tokens, int32_t num_q_heads,
-                                     int32_t num_kv_heads, int32_t head_dim, int32_t prefix_len, int32_t num_splits) {
-    if (batch <= 0 || max_seqlen <= 0 || total_tokens <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 ||
-        num_q_heads % num_kv_heads || prefix_len <= 0)
-        return 0;
-    int bps = 0;
-    const int splits =
-        prefix_splits(units_per_split(batch, num_kv_heads, max_seqlen, num_q_heads / num_kv_heads), prefix_len,
-                      num_splits, bps);
-    return workspace_bytes(total_tokens, num_q_heads, head_dim, splits);
-}
-
-int qattn_prefix_tree_fwd(const void* q, const int64_t q_stride[3], const void* k, const int64_t k_stride[3],
-                          const void* v, const int64_t v_stride[3], const void* k_prefix,
-                          const int64_t kp_stride[3], const void* v_prefix, const int64_t vp_stride[3],
-                          int32_t prefix_len, void* o, const int64_t o_stride[3], float* lse,
-                          const int64_t lse_stride[2], const int32_t* cu_seqlens, int32_t batch,
-                          int32_t max_seqlen, int64_t total_tokens, int64_t tree_seq_stride, int64_t tree_row0,
-                          int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, int32_t branching_factor,
-                          int32_t max_depth, float scale, int32_t dtype, void* workspace, int64_t workspace_size,
-                          int32_t num_splits, void* stream) {
-    clear_error();
+// Shared body of the two prefix entry points: parents null walks the heap
+// tree of branching_factor, else the explicit parent array.
+static int prefix_tree_impl(const void* q, const int64_t q_stride[3], const void* k, const int64_t k_stride[3],
+                            const void* v, const int64_t v_stride[3], const void* k_prefix,
+                            const int64_t kp_stride[3], const void* v_prefix, const int64_t vp_stride[3],
+                            int32_t prefix_len, void* o, const int64_t o_stride[3], float* lse,
+                            const int64_t lse_stride[2], const int32_t* cu_seqlens, const int32_t* parents,
+                            int32_t batch, int32_t max_seqlen, int64_t total_tokens, int64_t tree_seq_stride,
+                            int64_t tree_row0, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                            int32_t branching_factor, int32_t max_depth, float scale, int32_t dtype,
+                            void* workspace, int64_t workspace_size, int32_t num_splits, void* stream) {
     int rc = check_common(dtype, head_dim, batch, max_seqlen, total_tokens, num_q_heads, num_kv_heads, max_depth);
     if (rc) return rc;
     if (!(scale > 0.f)) {
@@ -675,8 +667,10 @@ int qattn_prefix_tree_fwd(const void* q, const int64_t q_stride[3], const void* 
     }
     tp.kv_seq_stride = tree_seq_stride;
     tp.kv_row0 = tree_row0;
+    tp.parents = parents;
+    const int walk = parents ? WALK_PARENTS : WALK_HEAP;
     hipStream_t st = (hipStream_t)stream;
-    if (prefix_len == 0) return run_tree(tp, dtype, head_dim, 0, 0, false, QATTN_ALGO_AUTO, st);
+    if (prefix_len == 0) return run_tree(tp, dtype, head_dim, walk, KV_PACKED, false, QATTN_ALGO_AUTO, st);
 
     if (!k_prefix || !v_prefix || !kp_stride || !vp_stride) {
         set_error("prefix pointers are null");
@@ -741,20 +735,72 @@ int qattn_prefix_tree_fwd(const void* q, const int64_t q_stride[3], const void* 
     pp.gdiv = make_divider(g);
     pp.scale_log2 = scale * kLog2e;
     if (dtype == QATTN_DTYPE_F16) {
-        rc = head_dim == 32   ? launch_prefix<F16, 32>(pp, tp, fused, st)
-             : head_dim == 64 ? launch_prefix<F16, 64>(pp, tp, fused, st)
-                              : launch_prefix<F16, 128>(pp, tp, fused, st);
+        rc = head_dim == 32   ? launch_prefix<F16, 32>(pp, tp, fused, walk, st)
+             : head_dim == 64 ? launch_prefix<F16, 64>(pp, tp, fused, walk, st)
+                              : launch_prefix<F16, 128>(pp, tp, fused, walk, st);
     } else {
-        rc = head_dim == 32   ? launch_prefix<BF16, 32>(pp, tp, fused, st)
-             : head_dim == 64 ? launch_prefix<BF16, 64>(pp, tp, fused, st)
-                              : launch_prefix<BF16, 128>(pp, tp, fused, st);
+        rc = head_dim == 32   ? launch_prefix<BF16, 32>(pp, tp, fused, walk, st)
+             : head_dim == 64 ? launch_prefix<BF16, 64>(pp, tp, fused, walk, st)
+                              : launch_prefix<BF16, 128>(pp, tp, fused, walk, st);
     }
     if (rc || fused) return rc;
     tp.part_m = pp.part_m;
     tp.part_l = pp.part_l;
     tp.part_acc = pp.part_acc;
     tp.n_split = splits;
-    return run_tree(tp, dtype, head_dim, 0, 0, true, QATTN_ALGO_AUTO, st);
+    return run_tree(tp, dtype, head_dim, walk, KV_PACKED, true, QATTN_ALGO_AUTO, st);
+}
+
+
+extern "C" {
+
+int64_t qattn_prefix_workspace_bytes(int32_t batch, int32_t max_seqlen, int64_t total_tokens, int32_t num_q_heads,
+                                     int32_t num_kv_heads, int32_t head_dim, int32_t prefix_len, int32_t num_splits) {
+    if (batch <= 0 || max_seqlen <= 0 || total_tokens <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 ||
+        num_q_heads % num_kv_heads || prefix_len <= 0)
+        return 0;
+    int bps = 0;
+    const int splits =
+        prefix_splits(units_per_split(batch, num_kv_heads, max_seqlen, num_q_heads / num_kv_heads), prefix_len,
+                      num_splits, bps);
+    return workspace_bytes(total_tokens, num_q_heads, head_dim, splits);
+}
+
+int qattn_prefix_tree_fwd(const void* q, const int64_t q_stride[3], const void* k, const int64_t k_stride[3],
+                          const void* v, const int64_t v_stride[3], const void* k_prefix,
+                          const int64_t kp_stride[3], const void* v_prefix, const int64_t vp_stride[3],
+                          int32_t prefix_len, void* o, const int64_t o_stride[3], float* lse,
+                          const int64_t lse_stride[2], const int32_t* cu_seqlens, int32_t batch,
+                          int32_t max_seqlen, int64_t total_tokens, int64_t tree_seq_stride, int64_t tree_row0,
+                          int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, int32_t branching_factor,
+                          int32_t max_depth, float scale, int32_t dtype, void* workspace, int64_t workspace_size,
+                          int32_t num_splits, void* stream) {
+    clear_error();
+    return prefix_tree_impl(q, q_stride, k, k_stride, v, v_stride, k_prefix, kp_stride, v_prefix, vp_stride,
+                            prefix_len, o, o_stride, lse, lse_stride, cu_seqlens, nullptr, batch, max_seqlen,
+                            total_tokens, tree_seq_stride, tree_row0, num_q_heads, num_kv_heads, head_dim,
+                            branching_factor, max_depth, scale, dtype, workspace, workspace_size, num_splits, stream);
+}
+
+int qattn_prefix_tree_parents_fwd(const void* q, const int64_t q_stride[3], const void* k,
+                                  const int64_t k_stride[3], const void* v, const int64_t v_stride[3],
+                                  const void* k_prefix, const int64_t kp_stride[3], const void* v_prefix,
+                                  const int64_t vp_stride[3], int32_t prefix_len, void* o,
+                                  const int64_t o_stride[3], float* lse, const int64_t lse_stride[2],
+                                  const int32_t* cu_seqlens, const int32_t* parents, int32_t batch,
+                                  int32_t max_seqlen, int64_t total_tokens, int64_t tree_seq_stride,
+                                  int64_t tree_row0, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                                  int32_t max_depth, float scale, int32_t dtype, void* workspace,
+                                  int64_t workspace_size, int32_t num_splits, void* stream) {
+    clear_error();
+    if (!parents && batch > 0 && max_seqlen > 0 && total_tokens > 0) {
+        set_error("parents is null");
+        return QATTN_ERR_ARG;
+    }
+    return prefix_tree_impl(q, q_stride, k, k_stride, v, v_stride, k_prefix, kp_stride, v_prefix, vp_stride,
+                            prefix_len, o, o_stride, lse, lse_stride, cu_seqlens, parents, batch, max_seqlen,
+                            total_tokens, tree_seq_stride, tree_row0, num_q_heads, num_kv_heads, head_dim, 1,
+                            max_depth, scale, dtype, workspace, workspace_size, num_splits, stream);
 }
 
 }  // extern "C"

@@ -329,6 +329,10 @@ static int dispatch_tree(const TreeParams& p, int walk, int layout, bool lse, bo
                    : launch_gather<T, D, WALK_HEAP, KV_PACKED, false, false>(p, st);
     }
     if (walk == WALK_PARENTS) {
+        if (pstate) {
+            return lse ? launch_gather<T, D, WALK_PARENTS, KV_PACKED, true, true>(p, st)
+                       : launch_gather<T, D, WALK_PARENTS, KV_PACKED, false, true>(p, st);
+        }
         return lse ? launch_gather<T, D, WALK_PARENTS, KV_PACKED, true, false>(p, st)
                    : launch_gather<T, D, WALK_PARENTS, KV_PACKED, false, false>(p, st);
     }

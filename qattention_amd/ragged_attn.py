@@ -331,9 +331,10 @@ def build_paged_kv(
 
 def _prefix_tree_forward(Q, K, V, cu_dev, B: int, max_seqlen: int, Kp, kp_stride, Vp, vp_stride,
                          prefix_len: int, branching_factor: int, max_depth: int, tree_seq_stride: int,
-                         tree_row0: int, want_lse: bool, num_splits: int = 0):
-    """Launch qattn_prefix_tree_fwd: MFMA prefix splits + ancestor walk, one
-    normalisation.  K/V hold the tree rows (addressed through cu_dev or
+                         tree_row0: int, want_lse: bool, num_splits: int = 0, parents=None):
+    """Launch qattn_prefix_tree_fwd (heap walk) or qattn_prefix_tree_parents_fwd
+    (parents given, a device int32 tensor): MFMA prefix splits + ancestor walk,
+    one normalisation.  K/V hold the tree rows (addressed through cu_dev or
     tree_seq_stride/tree_row0); Kp/Vp + 3 strides address the prefix rows."""
     device = Q.device
     T, Hq, D = Q.shape
@@ -345,17 +346,23 @@ def _prefix_tree_forward(Q, K, V, cu_dev, B: int, max_seqlen: int, Kp, kp_stride
     L = _lib.lib()
     ws_bytes = int(L.qattn_prefix_workspace_bytes(B, max_seqlen, T, Hq, Hkv, D, int(prefix_len), int(num_splits)))
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=device)
-    with torch.cuda.device(device):
-        rc = L.qattn_prefix_tree_fwd(
-            Q.data_ptr(), _lib.i64arr(Q.stride()), K.data_ptr(), _lib.i64arr(K.stride()),
+    head = (Q.data_ptr(), _lib.i64arr(Q.stride()), K.data_ptr(), _lib.i64arr(K.stride()),
             V.data_ptr(), _lib.i64arr(V.stride()), _lib.ptr(Kp), _lib.i64arr(kp_stride),
             _lib.ptr(Vp), _lib.i64arr(vp_stride), int(prefix_len),
             O.data_ptr(), _lib.i64arr(O.stride()), _lib.ptr(LSE),
-            _lib.i64arr(LSE.stride()) if LSE is not None else None,
-            cu_dev.data_ptr(), B, max_seqlen, T, int(tree_seq_stride), int(tree_row0),
-            Hq, Hkv, D, int(branching_factor), int(max_depth), 1.0 / math.sqrt(D), _dtype_code(Q),
-            ws.data_ptr(), ws_bytes, int(num_splits), _stream(device))
-    _lib.check(rc, "qattn_prefix_tree_fwd")
+            _lib.i64arr(LSE.stride()) if LSE is not None else None, cu_dev.data_ptr())
+    sizes = (B, max_seqlen, T, int(tree_seq_stride), int(tree_row0), Hq, Hkv, D)
+    tail = (ws.data_ptr(), ws_bytes, int(num_splits), _stream(device))
+    with torch.cuda.device(device):
+        if parents is None:
+            rc = L.qattn_prefix_tree_fwd(*head, *sizes, int(branching_factor), int(max_depth), 1.0 / math.sqrt(D),
+                                         _dtype_code(Q), *tail)
+            what = "qattn_prefix_tree_fwd"
+        else:
+            rc = L.qattn_prefix_tree_parents_fwd(*head, parents.data_ptr(), *sizes, int(max_depth),
+                                                 1.0 / math.sqrt(D), _dtype_code(Q), *tail)
+            what = "qattn_prefix_tree_parents_fwd"
+    _lib.check(rc, what)
     return O, LSE
 
 
@@ -402,6 +409,7 @@ def ragged_attention_prefix(
     max_seqlen: int = None,
     return_lse: bool = False,
     num_splits: int = 0,
+    parents: torch.Tensor = None,
 ):
     """Tree-verify attention over a prefix KV cache, GQA-native, in one pass.
 
@@ -413,7 +421,10 @@ def ragged_attention_prefix(
     Q: packed [T, Hq, D]; K, V: packed tree rows [T, Hkv, D]; cu_seqlens [B+1];
     K_prefix, V_prefix: [B, L, Hkv, D] per-sequence or [L, Hkv, D] shared by
     all sequences, any strides with a unit last dim (e.g. a permuted view of a
-    [B, Hkv, L, D] cache).  Returns O (and LSE [T, Hq] if return_lse)."""
+    [B, Hkv, L, D] cache).  parents (optional): int32 [T] sequence-local
+    parent of every token, roots self-looping, as in ragged_attention_with_parents
+    -- the EAGLE-3 dynamic tree of scripts/e2e_benchmark.py:1469-1474; then
+    branching_factor is ignored.  Returns O (and LSE [T, Hq] if return_lse)."""
     _check_dtypes(Q, K, V)
     assert K_prefix.dtype == Q.dtype and V_prefix.dtype == Q.dtype, "prefix dtype must match Q"
     device = _require_device(Q, K, V, K_prefix, V_prefix)
@@ -434,9 +445,14 @@ def ragged_attention_prefix(
     K_prefix, V_prefix = _vec(K_prefix), _vec(V_prefix)
     kp_stride = (0 if shared else K_prefix.stride(0), K_prefix.stride(1), K_prefix.stride(2))
     vp_stride = (0 if shared else V_prefix.stride(0), V_prefix.stride(1), V_prefix.stride(2))
+    par = None
+    if parents is not None:
+        if parents.numel() < T:
+            raise ValueError(f"parents has {parents.numel()} entries for {T} tokens")
+        par = parents.to(device=device, dtype=torch.int32, non_blocking=True).contiguous()
     O, LSE = _prefix_tree_forward(Q, K, V, cu_dev, B, ms, K_prefix if L else None, kp_stride,
                                   V_prefix if L else None, vp_stride, L, branching_factor, max_depth, 0, 0,
-                                  return_lse, num_splits)
+                                  return_lse, num_splits, par)
     return (O, LSE) if return_lse else O
 
 

@@ -325,3 +325,57 @@ def test_prefix_empty_and_zero_length_sequences():
     Kpe = torch.zeros(0, L, Hkv, D, dtype=torch.float16, device=DEV)
     O, LSE = ra.ragged_attention_prefix(Qe, Ke, Ke, cue, Kpe, Kpe, b, md, return_lse=True)
     assert O.shape == (0, Hq, D) and LSE.shape == (0, Hq)
+
+
+def _random_parents(lens, seed, window=None):
+    """Sequence-local parent arrays: the root self-loops, token i's parent is
+    drawn from [i - window, i) (or [0, i))."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for n in lens:
+        p = np.zeros(n, dtype=np.int32)
+        for i in range(1, n):
+            lo = 0 if window is None else max(0, i - window)
+            p[i] = rng.integers(lo, i)
+        out.append(p)
+    return np.concatenate(out) if out else np.zeros(0, dtype=np.int32)
+
+
+@pytest.mark.parametrize("lens,md,window,ns,Hq,Hkv", [
+    ([20, 33, 1], 7, 6, 0, 8, 2),
+    ([200, 300], 12, None, 1, 4, 4),
+    ([85, 0, 85], 3, None, 0, 32, 8),
+    ([64], 3, 2, 1, 4, 1),
+])
+def test_prefix_parents(lens, md, window, ns, Hq, Hkv):
+    """Prefix + explicit-parent tree in one call (the EAGLE-3 verify of
+    scripts/e2e_benchmark.py:1469-1496) against the oracle, through the split
+    path (0: automatic split count) and the fused single-split path (1)."""
+    ra = _ra()
+    D, L = 128, 700
+    say("prefix parents", lens, md, window, ns, Hq, Hkv)
+    Q, K, V, cu = make_inputs(lens, Hq, D, 6100 + md, Hkv=Hkv)
+    par = _random_parents(lens, 6101 + md, window)
+    Kp, Vp = _prefix(len(lens), L, Hkv, D, 6102 + md)
+    O, LSE = ra.ragged_attention_prefix(Q.to(DEV), K.to(DEV), V.to(DEV), cu, Kp.to(DEV), Vp.to(DEV), 2, md,
+                                        return_lse=True, num_splits=ns, parents=torch.from_numpy(par))
+    o_ref, lse_ref, _ = oracle_tree(Q, K, V, cu, 2, md, parents=par, Kp=Kp, Vp=Vp)
+    check_fp16(O.double().cpu().numpy(), o_ref, "prefix parents")
+    assert np.abs(LSE.double().cpu().numpy() - lse_ref).max() <= 1e-4
+
+
+@pytest.mark.parametrize("ns", [0, 1])
+def test_prefix_parents_equals_heap(ns):
+    """Heap-shaped parents ((i-1)//b, root self-loop) give the heap prefix
+    path's result."""
+    ra = _ra()
+    B, b, d, Hq, Hkv, D, L = 2, 4, 3, 8, 2, 128, 500
+    N = num_tree_nodes(b, d)
+    Q, K, V, cu = make_inputs([N] * B, Hq, D, 6200 + ns, Hkv=Hkv)
+    Kp, Vp = _prefix(B, L, Hkv, D, 6201 + ns)
+    par = np.array(([0] + [(i - 1) // b for i in range(1, N)]) * B, dtype=np.int32)
+    args = (Q.to(DEV), K.to(DEV), V.to(DEV), cu, Kp.to(DEV), Vp.to(DEV), b, d)
+    o_heap = ra.ragged_attention_prefix(*args, num_splits=ns)
+    o_par = ra.ragged_attention_prefix(*args, num_splits=ns, parents=torch.from_numpy(par))
+    err = float((o_heap.float() - o_par.float()).abs().max())
+    assert err <= 2e-3, f"heap vs parents: {err:.3e}"

@@ -127,6 +127,11 @@ def test_abi_prefix_stride_limits():
     assert call((512 * 256, -256, 64)) == -4
     assert call((512 * 256, (1 << 25) - 8, 64)) == -5
     assert call((512 * 256, 256, 64)) == -5
+    # the explicit-parents variant needs a parent array
+    kp = _lib.i64arr((512 * 256, 256, 64))
+    assert L.qattn_prefix_tree_parents_fwd(FAKE, ok3, FAKE, ok3, FAKE, ok3, FAKE, kp, FAKE, kp, 512, FAKE, ok3,
+                                           None, None, FAKE, None, 1, 15, 15, 0, 0, 4, 4, 64, 3, 0.125, 0,
+                                           None, 0, 0, None) == -1
 
 
 # ---------------------------------------------------------------------------
