@@ -1,6 +1,6 @@
 """Benchmark of the tree-verify attention hot path on one MI355X.
 
-    python bench.py [--steps K] [--warmup W] [--config cfg2|cfg3|cfg4|cfg5|gen1024] [--algo auto|gather|subtree]
+    python bench.py [--steps K] [--warmup W] [--config cfg2|cfg3|cfg4|cfg5|gen1024|cfg4_bhnd] [--algo auto|gather|subtree]
 
 A step is one full verify-attention call (all sequences, all heads, and the
 prefix KV cache when the config has one) over one batch of synthetic input,
@@ -52,6 +52,9 @@ CONFIGS = {
     "cfg4": dict(B=4, b=4, d=3, H=32, Hkv=8, D=128, L=10240, sigma=1.0),
     "cfg5": dict(B=16, b=8, d=4, H=32, Hkv=32, D=128, L=2048, sigma=0.5),
     "gen1024": dict(B=1, b=10, d=7, H=32, Hkv=32, D=128, L=0, sigma=1.0, N=1024, walk="parents"),
+    # cfg4 as the reference's E2E verify step holds it (scripts/e2e_benchmark.py:
+    # 1394-1502): Q [B, H, N, D], K/V [B, Hkv, L + N, D], one ragged_tree_attn call
+    "cfg4_bhnd": dict(B=4, b=4, d=3, H=32, Hkv=8, D=128, L=10240, sigma=1.0, layout="bhnd"),
 }
 
 
@@ -223,15 +226,25 @@ def main():
     nsets = args.sets or max(2, min(8, -(-600_000_000 // alg_bytes)))
 
     seed = B * 10000 + b * 100 + d
+    bhnd = c.get("layout") == "bhnd"
     sets = []
     for i in range(nsets):
-        sets.append([t.to(dev) if t is not None else None for t in make_set(c, seed + i, torch.float16)])
+        Q, K, V, Kp, Vp = make_set(c, seed + i, torch.float16)
+        if bhnd:
+            # the same values in the E2E layout: prefix rows then tree rows per sequence
+            Q = Q.view(B, N, H, D).permute(0, 2, 1, 3).contiguous()
+            K = torch.cat([Kp, K.view(B, N, Hkv, D)], 1).permute(0, 2, 1, 3).contiguous()
+            V = torch.cat([Vp, V.view(B, N, Hkv, D)], 1).permute(0, 2, 1, 3).contiguous()
+            Kp = Vp = None
+        sets.append([t.to(dev) if t is not None else None for t in (Q, K, V, Kp, Vp)])
     cu = torch.arange(0, (B + 1) * N, N, dtype=torch.int32, device=dev)
     parents = torch.tensor(heap_parents(b, N) * B, dtype=torch.int32, device=dev) if parents_walk else None
     torch.cuda.synchronize()
 
     def call(i):
         Q, K, V, Kp, Vp = sets[i]
+        if bhnd:
+            return ra.ragged_tree_attn(Q, K, V, b, d)
         if L:
             return ra.ragged_attention_prefix(Q, K, V, cu, Kp, Vp, b, d, max_seqlen=N)
         if parents_walk:
@@ -320,7 +333,8 @@ def main():
         "dtype": "f16",
         "data": f"synthetic N(0,{c['sigma']}^2), CPU-seeded (seed B*10000+b*100+d), {nsets} rotating sets",
         "config": {"workload": f"{args.config}: verify attention B={B} b={b} d={d} N={N} H={H} Hkv={Hkv} "
-                               f"D={D} L={L} fp16" + (", explicit parents" if parents_walk else ""), "B": B, "b": b, "d": d, "N": N, "H": H, "Hkv": Hkv,
+                               f"D={D} L={L} fp16" + (", explicit parents" if parents_walk else "")
+                               + (", [B, H, N, D] views" if bhnd else ""), "B": B, "b": b, "d": d, "N": N, "H": H, "Hkv": Hkv,
                    "D": D, "L": L, "tokens": T, "algo": args.algo},
         "achieved_GBps": round(achieved_bw / 1e9, 1),
         "wall_us_per_call": round(wall_us, 2),

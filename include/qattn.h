@@ -221,6 +221,49 @@ int qattn_prefix_tree_parents_fwd(const void *q, const int64_t q_stride[3],
                                   int32_t num_splits, void *stream);
 
 /*
+ * Tree verification over [B, H, N, D] views, as the model's attention layer
+ * holds them: no cu_seqlens, no packing, no copies.
+ *
+ * Replaces _ragged_tree_attn (scripts/e2e_benchmark.py:1394-1502): the
+ * prefix split and .contiguous() copies (:1430-1431), flash prefix attention
+ * with LSE (:1438-1448), the permute/contiguous repacks of Q and the tree K/V
+ * (:1455-1462), the cu arange (:1464), the tree kernel over a heap tree or
+ * over tree_parents (:1470-1478), the output permutes (:1482-1487) and
+ * fused_lse_merge (:1496) -- in one call, GQA-native.
+ *   q, o   [batch, num_q_heads, num_tree, head_dim], 4 element strides each
+ *          (torch order: batch, head, token, dim; stride_dim 1, rows and the
+ *          batch stride 16-byte aligned);
+ *   k, v   [batch, num_kv_heads, num_prefix + num_tree, head_dim], 4 strides:
+ *          rows 0 .. num_prefix-1 of each sequence are its prefix (all
+ *          visible to every tree token), the remaining num_tree rows its tree
+ *          tokens in BFS order.  For batch > 1 the batch stride of k and of v
+ *          must be the same positive multiple of its token stride (true of
+ *          any dense layout with the token dimension inside the batch one);
+ *   lse    null, or fp32 [batch, num_q_heads, num_tree] with 3 strides:
+ *          log-sum-exp over prefix and ancestors (natural log);
+ *   parents null: heap tree of branching_factor; else sequence-local parent
+ *          per tree token (the root its own parent, or negative) of sequence
+ *          s at parents[s * parents_stride + i] -- parents_stride 0 shares
+ *          one [num_tree] array (the reference's tree_parents) between all
+ *          sequences, num_tree gives one array per sequence.
+ * Query head h reads kv head h / (num_q_heads / num_kv_heads).  workspace as
+ * in qattn_prefix_tree_fwd, sized by qattn_prefix_workspace_bytes(batch,
+ * num_tree, batch * num_tree, num_q_heads, num_kv_heads, head_dim,
+ * num_prefix, num_splits); num_prefix 0 needs none.
+ */
+int qattn_ragged_tree_attn_fwd(const void *q, const int64_t q_stride[4],
+                               const void *k, const int64_t k_stride[4],
+                               const void *v, const int64_t v_stride[4],
+                               void *o, const int64_t o_stride[4],
+                               float *lse, const int64_t lse_stride[3],
+                               const int32_t *parents, int64_t parents_stride,
+                               int32_t batch, int32_t num_tree, int32_t num_prefix,
+                               int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                               int32_t branching_factor, int32_t max_depth, float scale,
+                               int32_t dtype, void *workspace, int64_t workspace_size,
+                               int32_t num_splits, void *stream);
+
+/*
  * Two-state softmax merge.
  *
  * Replaces _fused_lse_merge_kernel (src/ragged_attn.py:1575-1616) launched by

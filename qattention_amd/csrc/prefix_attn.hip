@@ -50,6 +50,7 @@ struct PrefixParams {
     int32_t n_split, blocks_per_split, qtiles, n_units;
     Divider gdiv;
     float scale_log2;
+    int64_t sq_b;  // uniform batch only: per-sequence q offset (as TreeParams::sq_b)
 };
 
 // 16-byte chunk swizzle of the K/V blocks in LDS: chunk c of key row r sits at
@@ -68,7 +69,7 @@ constexpr int kWaitVm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (
 
 // WALK: the tree walk of the fused epilogue (heap or explicit parents); the
 // split kernels leave the walk to the tree kernels.
-template <typename T, int D, bool FUSED, bool LSE, int WALK = WALK_HEAP>
+template <typename T, int D, bool FUSED, bool LSE, int WALK, bool BATCH>
 __global__ __launch_bounds__(kPrefixThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefix_attn_kernel(
     PrefixParams p, TreeParams tp) {
     constexpr int NC = D / 32;      // MFMA k-chunks over the head dim
@@ -102,7 +103,9 @@ __global__ __launch_bounds__(kPrefixThreads) __attribute__((amdgpu_waves_per_eu(
     const int kvh = r % p.Hkv;
     const int seq = r / p.Hkv;
 
-    const int32_t s0 = p.cu[seq], s1 = p.cu[seq + 1];
+    // (BATCH: a uniform batch of max_seqlen rows per sequence, no cu)
+    const int32_t s0 = BATCH ? seq * p.max_seqlen : p.cu[seq];
+    const int32_t s1 = BATCH ? s0 + p.max_seqlen : p.cu[seq + 1];
     if (s0 < 0 || s1 < s0 || (int64_t)s1 > p.total_tokens) return;
     int32_t n = s1 - s0;
     if (n > p.max_seqlen) n = p.max_seqlen;
@@ -135,7 +138,10 @@ __global__ __launch_bounds__(kPrefixThreads) __attribute__((amdgpu_waves_per_eu(
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
             qf[b][c] = Vec16{{0u, 0u, 0u, 0u}};
-            if (valid) qf[b][c] = ld16((const uint16_t*)p.q + qrow * p.sq_t + (int64_t)qh * p.sq_h + 32 * c + 8 * lq);
+            if (valid)
+                qf[b][c] = ld16((const uint16_t*)p.q + qrow * p.sq_t + (BATCH ? (int64_t)seq * p.sq_b : 0) +
+                                (int64_t)qh * p.sq_h +
+                                32 * c + 8 * lq);
         }
     }
 
@@ -470,7 +476,7 @@ __global__ __launch_bounds__(kPrefixThreads) __attribute__((amdgpu_waves_per_eu(
             // query grp's state is held by lane grp of the MFMA layout (l16 = grp, lq = 0)
             mw[b] = __shfl(m_run[b], grp);
             lw[b] = __shfl(l_tot[b], grp);
-            load_q4<D>(tp, qrb[b], hb[b], j, qf4[b]);
+            load_q4<D, BATCH>(tp, seq, qrb[b], hb[b], j, qf4[b]);
         }
         // Heap parents are monotonic, so walk step t of every token in the
         // tile's range [tl, th] lies in [par^t(tl), par^t(th)].  When those
@@ -561,7 +567,7 @@ __global__ __launch_bounds__(kPrefixThreads) __attribute__((amdgpu_waves_per_eu(
             // D = 64 up (two full chunks in flight spill registers there)
             constexpr int CH1 = 8 / NCH;
             constexpr int CHW = D >= 64 ? CH1 / 2 : CH1;
-            using W = Walk4<T, D, WALK, KV_PACKED, CHW>;
+            using W = Walk4<T, D, WALK, KV_PACKED, CHW, BATCH>;
             W w0(tp, seq, s0, n, tokb[0], kvh, j), w1(tp, seq, s0, n, tokb[1], kvh, j);
             w0.issue();
             w1.issue();
@@ -578,7 +584,7 @@ __global__ __launch_bounds__(kPrefixThreads) __attribute__((amdgpu_waves_per_eu(
         }
 #pragma unroll
         for (int b = 0; b < kQB; ++b)
-            if (vb[b]) write_out4<T, D, LSE>(tp, qrb[b], hb[b], j, mw[b], lw[b], acc[b]);
+            if (vb[b]) write_out4<T, D, LSE, BATCH>(tp, seq, qrb[b], hb[b], j, mw[b], lw[b], acc[b]);
     }
 }
 
@@ -609,6 +615,22 @@ static int64_t workspace_bytes(int64_t total_tokens, int hq, int head_dim, int s
     return 2 * align256(splits * plane * 4) + align256(splits * plane * head_dim * 4);
 }
 
+template <typename T, int D, bool BATCH>
+static void launch_prefix_b(const PrefixParams& pp, const TreeParams& tp, bool fused, int walk, dim3 g,
+                            hipStream_t st) {
+    const dim3 b(kPrefixThreads);
+    if (!fused)
+        hipLaunchKernelGGL((prefix_attn_kernel<T, D, false, false, WALK_HEAP, BATCH>), g, b, 0, st, pp, tp);
+    else if (walk == WALK_PARENTS && tp.lse)
+        hipLaunchKernelGGL((prefix_attn_kernel<T, D, true, true, WALK_PARENTS, BATCH>), g, b, 0, st, pp, tp);
+    else if (walk == WALK_PARENTS)
+        hipLaunchKernelGGL((prefix_attn_kernel<T, D, true, false, WALK_PARENTS, BATCH>), g, b, 0, st, pp, tp);
+    else if (tp.lse)
+        hipLaunchKernelGGL((prefix_attn_kernel<T, D, true, true, WALK_HEAP, BATCH>), g, b, 0, st, pp, tp);
+    else
+        hipLaunchKernelGGL((prefix_attn_kernel<T, D, true, false, WALK_HEAP, BATCH>), g, b, 0, st, pp, tp);
+}
+
 template <typename T, int D>
 static int launch_prefix(const PrefixParams& pp, const TreeParams& tp, bool fused, int walk, hipStream_t st) {
     const int64_t grid = ((int64_t)pp.n_units + 7) / 8 * 8;
@@ -616,17 +638,11 @@ static int launch_prefix(const PrefixParams& pp, const TreeParams& tp, bool fuse
         set_error("prefix grid too large");
         return QATTN_ERR_ARG;
     }
-    const dim3 g((unsigned)grid), b(kPrefixThreads);
-    if (!fused)
-        hipLaunchKernelGGL((prefix_attn_kernel<T, D, false, false>), g, b, 0, st, pp, tp);
-    else if (walk == WALK_PARENTS && tp.lse)
-        hipLaunchKernelGGL((prefix_attn_kernel<T, D, true, true, WALK_PARENTS>), g, b, 0, st, pp, tp);
-    else if (walk == WALK_PARENTS)
-        hipLaunchKernelGGL((prefix_attn_kernel<T, D, true, false, WALK_PARENTS>), g, b, 0, st, pp, tp);
-    else if (tp.lse)
-        hipLaunchKernelGGL((prefix_attn_kernel<T, D, true, true>), g, b, 0, st, pp, tp);
+    // (a null cu is a uniform batch: its addressing is compiled separately)
+    if (pp.cu)
+        launch_prefix_b<T, D, false>(pp, tp, fused, walk, dim3((unsigned)grid), st);
     else
-        hipLaunchKernelGGL((prefix_attn_kernel<T, D, true, false>), g, b, 0, st, pp, tp);
+        launch_prefix_b<T, D, true>(pp, tp, fused, walk, dim3((unsigned)grid), st);
     return launch_status("prefix_attn_kernel");
 }
 
@@ -634,8 +650,17 @@ static int launch_prefix(const PrefixParams& pp, const TreeParams& tp, bool fuse
 
 using namespace qattn;
 
-// Shared body of the two prefix entry points: parents null walks the heap
-// tree of branching_factor, else the explicit parent array.
+// Per-sequence offsets of a uniform batch of [B, H, N, D] views (no cu):
+// element offsets added to every q / o / lse row of sequence s (times s), and
+// the distance between the sequences' parent arrays.
+struct BatchView {
+    int64_t q_b, o_b, lse_b;
+    int32_t par_stride;
+};
+
+// Shared body of the prefix entry points: parents null walks the heap tree of
+// branching_factor, else the explicit parent array; bv null is the cu-packed
+// layout, else a uniform batch (cu_seqlens unused).
 static int prefix_tree_impl(const void* q, const int64_t q_stride[3], const void* k, const int64_t k_stride[3],
                             const void* v, const int64_t v_stride[3], const void* k_prefix,
                             const int64_t kp_stride[3], const void* v_prefix, const int64_t vp_stride[3],
@@ -644,7 +669,8 @@ static int prefix_tree_impl(const void* q, const int64_t q_stride[3], const void
                             int32_t batch, int32_t max_seqlen, int64_t total_tokens, int64_t tree_seq_stride,
                             int64_t tree_row0, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
                             int32_t branching_factor, int32_t max_depth, float scale, int32_t dtype,
-                            void* workspace, int64_t workspace_size, int32_t num_splits, void* stream) {
+                            void* workspace, int64_t workspace_size, int32_t num_splits, void* stream,
+                            const BatchView* bv) {
     int rc = check_common(dtype, head_dim, batch, max_seqlen, total_tokens, num_q_heads, num_kv_heads, max_depth);
     if (rc) return rc;
     if (!(scale > 0.f)) {
@@ -659,8 +685,16 @@ static int prefix_tree_impl(const void* q, const int64_t q_stride[3], const void
     if (batch == 0 || max_seqlen == 0 || total_tokens == 0) return QATTN_OK;
     TreeParams tp;
     rc = fill_tree_params(tp, q, q_stride, k, k_stride, v, v_stride, o, o_stride, lse, lse_stride, cu_seqlens, batch,
-                          max_seqlen, total_tokens, num_q_heads, num_kv_heads, branching_factor, max_depth, scale);
+                          max_seqlen, total_tokens, num_q_heads, num_kv_heads, branching_factor, max_depth, scale,
+                          bv != nullptr);
     if (rc) return rc;
+    if (bv) {
+        tp.cu = nullptr;
+        tp.sq_b = bv->q_b;
+        tp.so_b = bv->o_b;
+        tp.slse_b = bv->lse_b;
+        tp.par_stride = bv->par_stride;
+    }
     if (!row_aligned(k, k_stride, 2) || !row_aligned(v, v_stride, 2)) {
         set_error("k/v rows must be 16-byte aligned with stride_dim 1");
         return QATTN_ERR_LAYOUT;
@@ -707,7 +741,7 @@ static int prefix_tree_impl(const void* q, const int64_t q_stride[3], const void
     pp.q = q;
     pp.kp = k_prefix;
     pp.vp = v_prefix;
-    pp.cu = cu_seqlens;
+    pp.cu = tp.cu;
     if (!fused) {
         pp.part_m = (float*)workspace;
         pp.part_l = (float*)((char*)workspace + align256(splits * plane * 4));
@@ -715,6 +749,7 @@ static int prefix_tree_impl(const void* q, const int64_t q_stride[3], const void
     }
     pp.sq_t = q_stride[0];
     pp.sq_h = q_stride[1];
+    pp.sq_b = tp.sq_b;
     pp.skp_b = kp_stride[0];
     pp.skp_t = kp_stride[1];
     pp.skp_h = kp_stride[2];
@@ -779,7 +814,8 @@ int qattn_prefix_tree_fwd(const void* q, const int64_t q_stride[3], const void* 
     return prefix_tree_impl(q, q_stride, k, k_stride, v, v_stride, k_prefix, kp_stride, v_prefix, vp_stride,
                             prefix_len, o, o_stride, lse, lse_stride, cu_seqlens, nullptr, batch, max_seqlen,
                             total_tokens, tree_seq_stride, tree_row0, num_q_heads, num_kv_heads, head_dim,
-                            branching_factor, max_depth, scale, dtype, workspace, workspace_size, num_splits, stream);
+                            branching_factor, max_depth, scale, dtype, workspace, workspace_size, num_splits, stream,
+                            nullptr);
 }
 
 int qattn_prefix_tree_parents_fwd(const void* q, const int64_t q_stride[3], const void* k,
@@ -800,7 +836,68 @@ int qattn_prefix_tree_parents_fwd(const void* q, const int64_t q_stride[3], cons
     return prefix_tree_impl(q, q_stride, k, k_stride, v, v_stride, k_prefix, kp_stride, v_prefix, vp_stride,
                             prefix_len, o, o_stride, lse, lse_stride, cu_seqlens, parents, batch, max_seqlen,
                             total_tokens, tree_seq_stride, tree_row0, num_q_heads, num_kv_heads, head_dim, 1,
-                            max_depth, scale, dtype, workspace, workspace_size, num_splits, stream);
+                            max_depth, scale, dtype, workspace, workspace_size, num_splits, stream, nullptr);
+}
+
+int qattn_ragged_tree_attn_fwd(const void* q, const int64_t q_stride[4], const void* k, const int64_t k_stride[4],
+                               const void* v, const int64_t v_stride[4], void* o, const int64_t o_stride[4],
+                               float* lse, const int64_t lse_stride[3], const int32_t* parents,
+                               int64_t parents_stride, int32_t batch, int32_t num_tree, int32_t num_prefix,
+                               int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                               int32_t branching_factor, int32_t max_depth, float scale, int32_t dtype,
+                               void* workspace, int64_t workspace_size, int32_t num_splits, void* stream) {
+    clear_error();
+    if (!q_stride || !k_stride || !v_stride || !o_stride || (lse && !lse_stride)) {
+        set_error("null stride array");
+        return QATTN_ERR_ARG;
+    }
+    const int64_t total = (int64_t)batch * num_tree;
+    int rc = check_common(dtype, head_dim, batch, num_tree, total, num_q_heads, num_kv_heads, max_depth);
+    if (rc) return rc;
+    if (num_prefix < 0 || parents_stride < 0) {
+        set_error("bad num_prefix / parents_stride (%d, %lld)", num_prefix, (long long)parents_stride);
+        return QATTN_ERR_ARG;
+    }
+    if (batch == 0 || num_tree == 0) return QATTN_OK;
+    // (token, head, dim) strides of each tensor; a batch stride only matters
+    // when there is more than one sequence
+    const int64_t q3[3] = {q_stride[2], q_stride[1], q_stride[3]};
+    const int64_t o3[3] = {o_stride[2], o_stride[1], o_stride[3]};
+    const int64_t k3[3] = {k_stride[2], k_stride[1], k_stride[3]};
+    const int64_t v3[3] = {v_stride[2], v_stride[1], v_stride[3]};
+    const bool many = batch > 1;
+    const int64_t qb = many ? q_stride[0] : 0, ob = many ? o_stride[0] : 0;
+    const int64_t kb = many ? k_stride[0] : 0, vb = many ? v_stride[0] : 0;
+    if (qb % 8 || ob % 8) {
+        set_error("q/o batch strides must keep rows 16-byte aligned (multiples of 8 elements)");
+        return QATTN_ERR_LAYOUT;
+    }
+    // tree row n of sequence s is k/v row s * seq_rows + num_prefix + n
+    int64_t seq_rows = 1;  // one sequence: any non-zero value
+    if (many) {
+        if (kb <= 0 || k3[0] <= 0 || v3[0] <= 0 || kb % k3[0] || vb % v3[0] || kb / k3[0] != vb / v3[0]) {
+            set_error("k/v batch strides must be the same positive multiple of their token strides");
+            return QATTN_ERR_LAYOUT;
+        }
+        seq_rows = kb / k3[0];
+    }
+    if (parents && (int64_t)(batch - 1) * (many ? parents_stride : 0) + num_tree > INT32_MAX) {
+        set_error("parent array too large");
+        return QATTN_ERR_ARG;
+    }
+    BatchView bv;
+    bv.q_b = many ? qb - num_tree * q3[0] : 0;
+    bv.o_b = many ? ob - num_tree * o3[0] : 0;
+    bv.lse_b = lse && many ? lse_stride[0] - num_tree * lse_stride[2] : 0;
+    bv.par_stride = many ? (int32_t)parents_stride : 0;
+    const int64_t lse2[2] = {lse ? lse_stride[2] : 0, lse ? lse_stride[1] : 0};
+    // the prefix is rows 0 .. num_prefix - 1 of every sequence's k/v
+    const int64_t kp3[3] = {kb, k3[0], k3[1]};
+    const int64_t vp3[3] = {vb, v3[0], v3[1]};
+    return prefix_tree_impl(q, q3, k, k3, v, v3, k, kp3, v, vp3, num_prefix, o, o3, lse, lse ? lse2 : nullptr,
+                            nullptr, parents, batch, num_tree, total, seq_rows, num_prefix, num_q_heads,
+                            num_kv_heads, head_dim, parents ? 1 : branching_factor, max_depth, scale, dtype,
+                            workspace, workspace_size, num_splits, stream, &bv);
 }
 
 }  // extern "C"

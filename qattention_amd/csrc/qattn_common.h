@@ -56,7 +56,8 @@ struct TreeParams {
     const void* v;
     void* o;
     float* lse;
-    const int32_t* cu;          // [B+1] sequence offsets into q/o (and packed k/v)
+    const int32_t* cu;          // [B+1] sequence offsets into q/o (and packed k/v); null: uniform
+                                // batch, sequence s holds rows [s * max_seqlen, (s + 1) * max_seqlen)
     const int32_t* parents;     // explicit-parent walk: sequence-local parent per token
     const int32_t* page_table;  // paged K/V: [B, pt_cols] physical page per logical page
     int64_t sq_t, sq_h, sk_t, sk_h, sv_t, sv_h, so_t, so_h;
@@ -78,6 +79,13 @@ struct TreeParams {
     // every sequence's tree rows).
     int64_t kv_row0;            // extra row offset before the tree rows of each sequence
     int64_t kv_seq_stride;      // rows between consecutive sequences in k/v (0: use cu)
+    // Uniform batch only (null cu; kept last so the packed layout's fields
+    // keep their kernel-argument offsets): per-sequence element offsets added
+    // to the q / o / lse address of every row of sequence s (times s), and the
+    // parents of sequence s start at index s * par_stride (0: one array shared
+    // by every sequence; packed: at the sequence's first row).
+    int64_t sq_b, so_b, slse_b;
+    int32_t par_stride;
 };
 
 // Subtree tiling of a heap-indexed tree (levels of the BFS order).
@@ -133,7 +141,8 @@ int launch_stream(const TreeParams& p, const SubtreePlan& plan, int dtype, int h
 void set_error(const char* fmt, ...);
 void clear_error();
 
-// Host helpers shared by the entry points (tree_attn.hip).
+// Host helpers shared by the entry points (tree_attn.hip).  fill_tree_params
+// with uniform set takes a null cu (every sequence holds max_seqlen rows).
 bool row_aligned(const void* ptr, const int64_t* st, int n_outer);
 int check_common(int32_t dtype, int32_t head_dim, int32_t batch, int32_t max_seqlen, int64_t total_tokens,
                  int32_t hq, int32_t hkv, int32_t max_depth);
@@ -141,7 +150,7 @@ int launch_status(const char* what);
 int fill_tree_params(TreeParams& p, const void* q, const int64_t* qs, const void* k, const int64_t* ks,
                      const void* v, const int64_t* vs, void* o, const int64_t* os, float* lse, const int64_t* lss,
                      const int32_t* cu, int32_t batch, int32_t max_seqlen, int64_t total_tokens, int32_t hq,
-                     int32_t hkv, int32_t b, int32_t max_depth, float scale);
+                     int32_t hkv, int32_t b, int32_t max_depth, float scale, bool uniform = false);
 // walk: 0 heap, 1 parents; layout: 0 packed, 1 paged
 int run_tree(const TreeParams& p, int dtype, int head_dim, int walk, int layout, bool pstate, int algo,
              hipStream_t st);

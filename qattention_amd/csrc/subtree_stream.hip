@@ -293,7 +293,7 @@ __device__ __forceinline__ void tile_rowmap(const TreeParams& p, const Divider& 
 }
 
 // Issue the global loads of a tile into the staging registers.
-template <int D>
+template <int D, bool BATCH>
 __device__ __forceinline__ void tile_issue(const TreeParams& p, const TileMeta& t, const RowMap<D>& rm,
                                            Stage<D>& sg) {
     using Geo = StreamGeom<D>;
@@ -302,7 +302,8 @@ __device__ __forceinline__ void tile_issue(const TreeParams& p, const TileMeta& 
     const uint16_t* kg = (const uint16_t*)p.k + (t.kvb * p.sk_t + (int64_t)t.kvh * p.sk_h + c8);
     const uint16_t* vg = (const uint16_t*)p.v + (t.kvb * p.sv_t + (int64_t)t.kvh * p.sv_h + c8);
     const uint16_t* qg =
-        (const uint16_t*)p.q + ((int64_t)t.start * p.sq_t + (int64_t)t.kvh * p.group * p.sq_h + c8);
+        (const uint16_t*)p.q +
+        ((int64_t)t.start * p.sq_t + (BATCH ? (int64_t)t.seq * p.sq_b : 0) + (int64_t)t.kvh * p.group * p.sq_h + c8);
 #pragma unroll
     for (int ps = 0; ps < Geo::PASSES; ++ps) {
         if (ps * Geo::RPP >= t.rows) break;  // wave-uniform
@@ -395,7 +396,7 @@ __device__ __forceinline__ void build_query_table(const TreeParams& p, const Div
 }
 
 // One wave: attention of 16 queries (query block qb) of the tile held in LDS.
-template <typename T, int D, bool LSE, bool PSTATE>
+template <typename T, int D, bool LSE, bool PSTATE, bool BATCH>
 __device__ __forceinline__ void block_compute(const TreeParams& p, const TileMeta& t, int qb, const uint16_t* Ks,
                                               const uint16_t* Vs, const uint16_t* Qs, const QueryEntry* qt) {
     using Geo = StreamGeom<D>;
@@ -558,14 +559,17 @@ __device__ __forceinline__ void block_compute(const TreeParams& p, const TileMet
     const float l_safe = (l == 0.f) ? 1.f : l;  // src/ragged_attn.py:379-380
     const float inv = __builtin_amdgcn_rcpf(l_safe);
     if constexpr (LSE) {
-        if (qvalid && i4 == 0) p.lse[qrow * p.slse_t + (int64_t)qh * p.slse_h] = (m + fast_log2(l_safe)) * kLn2;
+        if (qvalid && i4 == 0)
+            p.lse[qrow * p.slse_t + (BATCH ? (int64_t)t.seq * p.slse_b : 0) + (int64_t)qh * p.slse_h] =
+                (m + fast_log2(l_safe)) * kLn2;
     }
 
     // ---- O: lane holds O^T[16 dt + 4 i4 + r][c16], stored straight as 8-byte
     // pieces; the 4 lanes of a column fill 32 contiguous bytes per d-tile and
     // the d-tiles complete the row in L2 ----
     if (qvalid) {
-        uint16_t* optr = (uint16_t*)p.o + qrow * p.so_t + (int64_t)qh * p.so_h + 4 * i4;
+        uint16_t* optr =
+            (uint16_t*)p.o + qrow * p.so_t + (BATCH ? (int64_t)t.seq * p.so_b : 0) + (int64_t)qh * p.so_h + 4 * i4;
 #pragma unroll
         for (int dt = 0; dt < ND; ++dt) {
             *reinterpret_cast<uint2*>(optr + 16 * dt) =
@@ -575,12 +579,12 @@ __device__ __forceinline__ void block_compute(const TreeParams& p, const TileMet
     }
 }
 
-template <typename T, int D, bool LSE, bool PSTATE>
+template <typename T, int D, bool LSE, bool PSTATE, bool BATCH>
 __device__ __forceinline__ void tile_compute(const TreeParams& p, const TileMeta& t, const uint16_t* Ks,
                                              const uint16_t* Vs, const uint16_t* Qs, const QueryEntry* qt) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     for (int qb = wave; 16 * qb < t.nq; qb += kStThreads / 64)
-        block_compute<T, D, LSE, PSTATE>(p, t, qb, Ks, Vs, Qs, qt);
+        block_compute<T, D, LSE, PSTATE, BATCH>(p, t, qb, Ks, Vs, Qs, qt);
 }
 
 // Next item of a group: one returning atomic on the group's counter.
@@ -599,7 +603,9 @@ __device__ __forceinline__ uint32_t sched_grab(uint32_t* ctr) {
 // fewer items.  Every workgroup that took part adds one to the group's done
 // counter after its last request, and the last of them clears both counters,
 // so the next launch finds them at zero.
-template <typename T, int D, bool LSE, bool PSTATE>
+// BATCH: a uniform batch (null cu, per-sequence q/o/lse offsets); the packed
+// layout compiles without that addressing.
+template <typename T, int D, bool LSE, bool PSTATE, bool BATCH>
 __global__ __launch_bounds__(kStThreads)
 __attribute__((amdgpu_waves_per_eu(3, 3))) void tree_stream_kernel(
     TreeParams p, SubtreePlan plan, StreamArgs sa) {
@@ -655,13 +661,16 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void tree_stream_kernel(
     RowMap<D> rm;
     Stage<D> sg;
     const int seq0 = tile_seq(sa, w);  // < p.B: w < n_work
-    const int32_t cu_mine = threadIdx.x <= p.B ? p.cu[threadIdx.x] : 0;  // p.B < kCuCache = kStThreads
-    const int32_t s0 = __builtin_amdgcn_readfirstlane(p.cu[seq0]);
-    const int32_t e0 = __builtin_amdgcn_readfirstlane(p.cu[seq0 + 1]);
+    // (a uniform batch holds max_seqlen rows per sequence)
+    const int32_t cu_mine = threadIdx.x > p.B ? 0
+                            : BATCH        ? (int32_t)threadIdx.x * p.max_seqlen
+                                           : p.cu[threadIdx.x];  // p.B < kCuCache = kStThreads
+    const int32_t s0 = BATCH ? seq0 * p.max_seqlen : __builtin_amdgcn_readfirstlane(p.cu[seq0]);
+    const int32_t e0 = BATCH ? s0 + p.max_seqlen : __builtin_amdgcn_readfirstlane(p.cu[seq0 + 1]);
     tile_setup_se<D>(p, plan, sa, w, s0, e0, none, cur, band_tb, band_pk);
     if (cur.valid) {
         tile_rowmap<D>(p, gdiv, cur, rm);
-        tile_issue<D>(p, cur, rm, sg);
+        tile_issue<D, BATCH>(p, cur, rm, sg);
         // the first query table is built while the first loads are in flight
         // (the first loop top's barrier publishes it)
         build_query_table(p, gdiv, cur, qtab);
@@ -690,7 +699,7 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void tree_stream_kernel(
             const bool fresh = tile_setup<D>(p, plan, sa, cu_lds, wn, cur, nxt, band_tb, band_pk);
             if (nxt.valid) {
                 if (fresh) tile_rowmap<D>(p, gdiv, nxt, rm);
-                tile_issue<D>(p, nxt, rm, sg);
+                tile_issue<D, BATCH>(p, nxt, rm, sg);
             }
         }
         // the next item, or (after this workgroup's last request) done
@@ -703,7 +712,7 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void tree_stream_kernel(
                 tab_n = cur.n;
                 __syncthreads();
             }
-            tile_compute<T, D, LSE, PSTATE>(p, cur, Ks, Vs, Qs, qtab);
+            tile_compute<T, D, LSE, PSTATE, BATCH>(p, cur, Ks, Vs, Qs, qtab);
         }
         __syncthreads();
         if (!more) break;
@@ -762,7 +771,7 @@ static uint32_t* sched_counters(int dev, hipStream_t st) {
     return pool[dev] + 2 * slot;
 }
 
-template <typename T, int D, bool LSE, bool PSTATE>
+template <typename T, int D, bool LSE, bool PSTATE, bool BATCH>
 static int launch_stream_t(const TreeParams& p, const SubtreePlan& plan, hipStream_t st) {
     using Geo = StreamGeom<D>;
     const int64_t n_work = (int64_t)p.B * p.Hkv * plan.total_tiles;
@@ -776,7 +785,7 @@ static int launch_stream_t(const TreeParams& p, const SubtreePlan& plan, hipStre
         return QATTN_ERR_ARG;
     }
     const size_t lds = Geo::LDS_BYTES;
-    auto kern = tree_stream_kernel<T, D, LSE, PSTATE>;
+    auto kern = tree_stream_kernel<T, D, LSE, PSTATE, BATCH>;
     int dev = 0, cus = 0, per_cu = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
@@ -813,10 +822,14 @@ static int launch_stream_t(const TreeParams& p, const SubtreePlan& plan, hipStre
 
 int launch_stream(const TreeParams& p, const SubtreePlan& plan, int dtype, int head_dim, bool pstate,
                   hipStream_t st) {
-#define QATTN_STREAM_D(T, D)                                                                  \
-    if (p.lse) return pstate ? launch_stream_t<T, D, true, true>(p, plan, st)                  \
-                             : launch_stream_t<T, D, true, false>(p, plan, st);                \
-    return pstate ? launch_stream_t<T, D, false, true>(p, plan, st) : launch_stream_t<T, D, false, false>(p, plan, st);
+#define QATTN_STREAM_B(T, D, B)                                                                \
+    if (p.lse) return pstate ? launch_stream_t<T, D, true, true, B>(p, plan, st)                \
+                             : launch_stream_t<T, D, true, false, B>(p, plan, st);              \
+    return pstate ? launch_stream_t<T, D, false, true, B>(p, plan, st)                          \
+                  : launch_stream_t<T, D, false, false, B>(p, plan, st);
+#define QATTN_STREAM_D(T, D)               \
+    if (!p.cu) { QATTN_STREAM_B(T, D, true) } \
+    QATTN_STREAM_B(T, D, false)
     if (dtype == QATTN_DTYPE_F16) {
         if (head_dim == 32) { QATTN_STREAM_D(F16, 32) }
         if (head_dim == 64) { QATTN_STREAM_D(F16, 64) }
@@ -826,6 +839,7 @@ int launch_stream(const TreeParams& p, const SubtreePlan& plan, int dtype, int h
     if (head_dim == 64) { QATTN_STREAM_D(BF16, 64) }
     QATTN_STREAM_D(BF16, 128)
 #undef QATTN_STREAM_D
+#undef QATTN_STREAM_B
 }
 
 }  // namespace qattn

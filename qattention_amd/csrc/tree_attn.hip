@@ -51,7 +51,7 @@ void clear_error() { g_err[0] = 0; }
 // Gather kernel: 4 lanes per (token, q head), 64 pairs per workgroup with the
 // head index fastest, so a workgroup reads 2 tokens' contiguous head rows.
 // ---------------------------------------------------------------------------
-template <typename T, int D, int WALK, int LAYOUT, bool LSE, bool PSTATE>
+template <typename T, int D, int WALK, int LAYOUT, bool LSE, bool PSTATE, bool BATCH>
 __global__ __launch_bounds__(kThreads) void tree_gather_kernel(TreeParams p) {
     constexpr int NCH = D / 32;
     constexpr int SLOTS = kThreads / 4;
@@ -63,15 +63,15 @@ __global__ __launch_bounds__(kThreads) void tree_gather_kernel(TreeParams p) {
     const int seq = (int)(rest / p.max_seqlen);
     if (seq >= p.B) return;
     int32_t start, n;
-    if (!seq_bounds(p, seq, start, n)) return;
+    if (!seq_bounds<BATCH>(p, seq, start, n)) return;
     if (tok >= n) return;
     const int64_t qrow = (int64_t)start + tok;
     Vec16 qf[NCH];
-    load_q4<D>(p, qrow, h, j, qf);
+    load_q4<D, BATCH>(p, seq, qrow, h, j, qf);
     float m = -INFINITY, l = 0.f, acc[8 * NCH];
     // the first chunk of the walk's K/V loads is in flight while the prefix
     // splits are merged (the walk does not depend on them)
-    Walk4<T, D, WALK, LAYOUT> w(p, seq, start, n, tok, h / p.group, j);
+    Walk4<T, D, WALK, LAYOUT, 8 / (D / 32), BATCH> w(p, seq, start, n, tok, h / p.group, j);
     w.issue();
     if constexpr (PSTATE) {
         load_partial_state4<D>(p, qrow, h, j, m, l, acc);
@@ -84,7 +84,7 @@ __global__ __launch_bounds__(kThreads) void tree_gather_kernel(TreeParams p) {
         w.issue();
         w.fold(qf, m, l, acc);
     }
-    write_out4<T, D, LSE>(p, qrow, h, j, m, l, acc);
+    write_out4<T, D, LSE, BATCH>(p, seq, qrow, h, j, m, l, acc);
 }
 
 // ---------------------------------------------------------------------------
@@ -100,11 +100,12 @@ __global__ __launch_bounds__(kThreads) void ancestors_kernel(TreeParams p, int32
     if (!seq_bounds(p, seq, start, n)) return;
     if (tok >= n) return;
     int32_t* row = out + ((int64_t)start + tok) * (p.max_depth + 1);
+    const int32_t pb = parents_base(p, seq, start);
     int32_t cur = tok, prev = -1;
     for (int s = 0; s <= p.max_depth; ++s) {
         row[s] = (cur != prev) ? cur : -1;
         prev = cur;
-        cur = walk_next<WALK>(p, start, n, cur);
+        cur = walk_next<WALK>(p, pb, n, cur);
     }
 }
 
@@ -282,7 +283,7 @@ static bool make_subtree_plan(int b, int64_t n, int max_depth, int rcap, int nca
     return rows <= rcap;
 }
 
-template <typename T, int D, int WALK, int LAYOUT, bool LSE, bool PSTATE>
+template <typename T, int D, int WALK, int LAYOUT, bool LSE, bool PSTATE, bool BATCH = false>
 static int launch_gather(const TreeParams& p, hipStream_t st) {
     constexpr int SLOTS = kThreads / 4;  // 4 lanes per (token, q head)
     const int64_t slots = (int64_t)p.B * p.max_seqlen * p.Hq;
@@ -291,9 +292,19 @@ static int launch_gather(const TreeParams& p, hipStream_t st) {
         set_error("grid too large (%lld blocks)", (long long)blocks);
         return QATTN_ERR_ARG;
     }
-    hipLaunchKernelGGL((tree_gather_kernel<T, D, WALK, LAYOUT, LSE, PSTATE>), dim3((unsigned)blocks),
+    hipLaunchKernelGGL((tree_gather_kernel<T, D, WALK, LAYOUT, LSE, PSTATE, BATCH>), dim3((unsigned)blocks),
                        dim3(kThreads), 0, st, p);
     return launch_status("tree_gather_kernel");
+}
+
+template <typename T, int D, int WALK, bool BATCH>
+static int gather_packed(const TreeParams& p, bool lse, bool pstate, hipStream_t st) {
+    if (pstate) {
+        return lse ? launch_gather<T, D, WALK, KV_PACKED, true, true, BATCH>(p, st)
+                   : launch_gather<T, D, WALK, KV_PACKED, false, true, BATCH>(p, st);
+    }
+    return lse ? launch_gather<T, D, WALK, KV_PACKED, true, false, BATCH>(p, st)
+               : launch_gather<T, D, WALK, KV_PACKED, false, false, BATCH>(p, st);
 }
 
 template <typename T, int D>
@@ -320,21 +331,14 @@ static int dispatch_tree(const TreeParams& p, int walk, int layout, bool lse, bo
         set_error("the subtree kernel supports the heap walk on packed K/V only");
         return QATTN_ERR_ARG;
     }
-    if (walk == WALK_HEAP && layout == KV_PACKED) {
-        if (pstate) {
-            return lse ? launch_gather<T, D, WALK_HEAP, KV_PACKED, true, true>(p, st)
-                       : launch_gather<T, D, WALK_HEAP, KV_PACKED, false, true>(p, st);
+    if (layout == KV_PACKED) {
+        // (a null cu is a uniform batch: its addressing is compiled separately)
+        if (!p.cu) {
+            return walk == WALK_HEAP ? gather_packed<T, D, WALK_HEAP, true>(p, lse, pstate, st)
+                                     : gather_packed<T, D, WALK_PARENTS, true>(p, lse, pstate, st);
         }
-        return lse ? launch_gather<T, D, WALK_HEAP, KV_PACKED, true, false>(p, st)
-                   : launch_gather<T, D, WALK_HEAP, KV_PACKED, false, false>(p, st);
-    }
-    if (walk == WALK_PARENTS) {
-        if (pstate) {
-            return lse ? launch_gather<T, D, WALK_PARENTS, KV_PACKED, true, true>(p, st)
-                       : launch_gather<T, D, WALK_PARENTS, KV_PACKED, false, true>(p, st);
-        }
-        return lse ? launch_gather<T, D, WALK_PARENTS, KV_PACKED, true, false>(p, st)
-                   : launch_gather<T, D, WALK_PARENTS, KV_PACKED, false, false>(p, st);
+        return walk == WALK_HEAP ? gather_packed<T, D, WALK_HEAP, false>(p, lse, pstate, st)
+                                 : gather_packed<T, D, WALK_PARENTS, false>(p, lse, pstate, st);
     }
     return lse ? launch_gather<T, D, WALK_HEAP, KV_PAGED, true, false>(p, st)
                : launch_gather<T, D, WALK_HEAP, KV_PAGED, false, false>(p, st);
@@ -361,9 +365,10 @@ int run_tree(const TreeParams& p, int dtype, int head_dim, int walk, int layout,
 int fill_tree_params(TreeParams& p, const void* q, const int64_t* qs, const void* k, const int64_t* ks,
                      const void* v, const int64_t* vs, void* o, const int64_t* os, float* lse,
                      const int64_t* lss, const int32_t* cu, int32_t batch, int32_t max_seqlen,
-                     int64_t total_tokens, int32_t hq, int32_t hkv, int32_t b, int32_t max_depth, float scale) {
+                     int64_t total_tokens, int32_t hq, int32_t hkv, int32_t b, int32_t max_depth, float scale,
+                     bool uniform) {
     p = TreeParams{};
-    if (!q || !qs || !k || !ks || !v || !vs || !o || !os || !cu || (lse && !lss)) {
+    if (!q || !qs || !k || !ks || !v || !vs || !o || !os || (!cu && !uniform) || (lse && !lss)) {
         set_error("null pointer argument");
         return QATTN_ERR_ARG;
     }

@@ -20,7 +20,15 @@ enum { KV_PACKED = 0, KV_PAGED = 1 };
 __device__ __forceinline__ int rl(int v, int i) { return __builtin_amdgcn_readlane(v, i); }
 
 // Sequence bounds with the guards documented in qattn.h.
+// BATCH (a uniform batch, null cu): sequence seq holds rows
+// [seq * max_seqlen, (seq + 1) * max_seqlen).
+template <bool BATCH = false>
 __device__ __forceinline__ bool seq_bounds(const TreeParams& p, int seq, int32_t& start, int32_t& n) {
+    if constexpr (BATCH) {
+        start = seq * p.max_seqlen;
+        n = p.max_seqlen;
+        return true;
+    }
     int32_t s = p.cu[seq], e = p.cu[seq + 1];
     if (s < 0 || e < s || (int64_t)e > p.total_tokens) return false;
     start = s;
@@ -35,21 +43,31 @@ __device__ __forceinline__ int64_t kv_base(const TreeParams& p, int seq, int32_t
     return p.kv_seq_stride ? (int64_t)seq * p.kv_seq_stride + p.kv_row0 : (int64_t)start;
 }
 
-// Next node of the walk (src/ragged_attn.py:376-377 heap, :692-694 parents).
+// Index of a sequence's first entry in the parent array: its first row
+// (packed by cu), or seq * par_stride (uniform batch; stride 0 shares one
+// array between all sequences).
+template <bool BATCH = false>
+__device__ __forceinline__ int32_t parents_base(const TreeParams& p, int seq, int32_t start) {
+    return BATCH ? seq * p.par_stride : start;
+}
+
+// Next node of the walk (src/ragged_attn.py:376-377 heap, :692-694 parents);
+// pb is the sequence's parents_base.
 template <int WALK>
-__device__ __forceinline__ int32_t walk_next(const TreeParams& p, int32_t start, int32_t n, int32_t cur) {
+__device__ __forceinline__ int32_t walk_next(const TreeParams& p, int32_t pb, int32_t n, int32_t cur) {
     if constexpr (WALK == WALK_HEAP) {
         return heap_parent(cur, p.bdiv);
     } else {
-        const int32_t par = p.parents[start + cur];
+        const int32_t par = p.parents[pb + cur];
         return (par >= 0 && par < n) ? par : cur;
     }
 }
 
 // Q fragment of a query in the 4-lane layout.
-template <int D>
-__device__ __forceinline__ void load_q4(const TreeParams& p, int64_t qrow, int h, int j, Vec16* qf) {
-    const uint16_t* qp = (const uint16_t*)p.q + qrow * p.sq_t + (int64_t)h * p.sq_h + 8 * j;
+template <int D, bool BATCH = false>
+__device__ __forceinline__ void load_q4(const TreeParams& p, int seq, int64_t qrow, int h, int j, Vec16* qf) {
+    const uint16_t* qp = (const uint16_t*)p.q + qrow * p.sq_t + (BATCH ? (int64_t)seq * p.sq_b : 0) +
+                         (int64_t)h * p.sq_h + 8 * j;
 #pragma unroll
     for (int i = 0; i < D / 32; ++i) qf[i] = ld16(qp + 32 * i);
 }
@@ -166,13 +184,13 @@ __device__ __forceinline__ void fold_scores(const float* s, const Vec16 (*vf)[NC
 // the walk stops once every lane's walk has stalled (root reached or
 // self-loop).  A caller may issue the first chunk before it builds the
 // initial state, so those loads overlap its own.
-template <typename T, int D, int WALK, int LAYOUT, int CH_ = 8 / (D / 32)>
+template <typename T, int D, int WALK, int LAYOUT, int CH_ = 8 / (D / 32), bool BATCH = false>
 struct Walk4 {
     static constexpr int NCH = D / 32;
     static constexpr int CH = CH_;  // default 2 steps at D=128: 64 VGPRs of K/V loads in flight per lane
     const TreeParams& p;
     const int seq;
-    const int32_t start, n;
+    const int32_t pb, n;  // parents_base of the sequence, its length
     const int64_t kvb;
     const uint16_t* kb;
     const uint16_t* vb;
@@ -183,7 +201,7 @@ struct Walk4 {
 
     __device__ __forceinline__ Walk4(const TreeParams& p_, int seq_, int32_t start_, int32_t n_, int tok, int kvh,
                                      int j)
-        : p(p_), seq(seq_), start(start_), n(n_), kvb(kv_base(p_, seq_, start_)),
+        : p(p_), seq(seq_), pb(parents_base<BATCH>(p_, seq_, start_)), n(n_), kvb(kv_base(p_, seq_, start_)),
           kb((const uint16_t*)p_.k + (int64_t)kvh * p_.sk_h + 8 * j),
           vb((const uint16_t*)p_.v + (int64_t)kvh * p_.sv_h + 8 * j), cur(tok), prev(-1), s0(0) {}
 
@@ -207,7 +225,7 @@ struct Walk4 {
             }
             val[t] = ok;
             prev = cur;
-            cur = walk_next<WALK>(p, start, n, cur);
+            cur = walk_next<WALK>(p, pb, n, cur);
         }
 #pragma unroll
         for (int t = 0; t < CH; ++t) {
@@ -238,26 +256,17 @@ struct Walk4 {
     __device__ __forceinline__ bool more() const { return s0 <= p.max_depth && __any(cur != prev); }
 };
 
-template <typename T, int D, int WALK, int LAYOUT>
-__device__ __forceinline__ void gather_walk4(const TreeParams& p, int seq, int32_t start, int32_t n, int tok,
-                                             int kvh, const Vec16* qf, int j, float& m, float& l, float* acc) {
-    Walk4<T, D, WALK, LAYOUT> w(p, seq, start, n, tok, kvh, j);
-    do {
-        w.issue();
-        w.fold(qf, m, l, acc);
-    } while (w.more());
-}
-
 // Normalise and store one query's output (+ LSE from lane 0 of the group).
-template <typename T, int D, bool LSE>
-__device__ __forceinline__ void write_out4(const TreeParams& p, int64_t qrow, int h, int j, float m, float l,
-                                           float* acc) {
+template <typename T, int D, bool LSE, bool BATCH = false>
+__device__ __forceinline__ void write_out4(const TreeParams& p, int seq, int64_t qrow, int h, int j, float m,
+                                           float l, float* acc) {
     constexpr int NCH = D / 32;
     // l == 0 only for a query with no attended key; the reference divides by 1
     // there (src/ragged_attn.py:379-380).
     const float l_safe = (l == 0.f) ? 1.f : l;
     const float inv = __builtin_amdgcn_rcpf(l_safe);
-    uint16_t* optr = (uint16_t*)p.o + qrow * p.so_t + (int64_t)h * p.so_h + 8 * j;
+    uint16_t* optr =
+        (uint16_t*)p.o + qrow * p.so_t + (BATCH ? (int64_t)seq * p.so_b : 0) + (int64_t)h * p.so_h + 8 * j;
 #pragma unroll
     for (int i = 0; i < NCH; ++i) {
         float r[8];
@@ -266,7 +275,9 @@ __device__ __forceinline__ void write_out4(const TreeParams& p, int64_t qrow, in
         st16(optr + 32 * i, pack8<T>(r));
     }
     if constexpr (LSE) {
-        if (j == 0) p.lse[qrow * p.slse_t + (int64_t)h * p.slse_h] = (m + fast_log2(l_safe)) * kLn2;
+        if (j == 0)
+            p.lse[qrow * p.slse_t + (BATCH ? (int64_t)seq * p.slse_b : 0) + (int64_t)h * p.slse_h] =
+                (m + fast_log2(l_safe)) * kLn2;
     }
 }
 

@@ -456,6 +456,76 @@ def ragged_attention_prefix(
     return (O, LSE) if return_lse else O
 
 
+def ragged_tree_attn(
+    Q: torch.Tensor,
+    K: torch.Tensor,
+    V: torch.Tensor,
+    branching_factor: int,
+    max_depth: int,
+    tree_parents: Optional[torch.Tensor] = None,
+    return_lse: bool = False,
+    num_splits: int = 0,
+):
+    """EAGLE-3 tree verification over the attention layer's own [B, H, N, D]
+    tensors, in one launch sequence with no copies: the replacement for
+    _ragged_tree_attn (scripts/e2e_benchmark.py:1394-1502), same arguments
+    and result.
+
+    Q: [B, Hq, N_q, D]; K, V: [B, Hkv, N_kv, D] with N_kv = N_prefix + N_q
+    (each sequence's prefix rows, visible to every tree token, then its tree
+    tokens in BFS order); Hkv may divide Hq (GQA, no repeat_kv needed).  Any
+    strides with a unit last dim work in place (permuted views, slices of a
+    larger cache).  tree_parents: int32 [N_q] sequence-local parents shared
+    by every sequence (the reference's case, :1470) or [B, N_q] one tree per
+    sequence; the root is its own parent.  Otherwise the heap tree of
+    branching_factor is walked (:1475-1478).  Returns O [B, Hq, N_q, D] (and
+    LSE [B, Hq, N_q] fp32, natural log, if return_lse)."""
+    _check_dtypes(Q, K, V)
+    device = _require_device(Q, K, V)
+    if Q.dim() != 4 or K.dim() != 4 or V.dim() != 4 or K.shape != V.shape:
+        raise ValueError(f"expected [B, H, N, D] tensors: Q {tuple(Q.shape)} K {tuple(K.shape)} V {tuple(V.shape)}")
+    B, Hq, N, D = Q.shape
+    Hkv, N_kv = K.shape[1], K.shape[2]
+    if K.shape[0] != B or K.shape[3] != D or N_kv < N:
+        raise ValueError(f"K/V {tuple(K.shape)} incompatible with Q {tuple(Q.shape)}")
+    if Hkv < 1 or Hq % Hkv:
+        raise ValueError(f"num q heads {Hq} must be a multiple of num kv heads {Hkv}")
+    L = N_kv - N
+    Q = _vec(Q)
+    K, V = _vec(K), _vec(V)
+    if B > 1:
+        # the kernels place sequence s's k/v rows at s * (batch stride / token
+        # stride): both tensors need the same whole-row batch stride
+        kr = K.stride(0) // K.stride(2) if K.stride(2) > 0 and K.stride(0) % K.stride(2) == 0 else -1
+        vr = V.stride(0) // V.stride(2) if V.stride(2) > 0 and V.stride(0) % V.stride(2) == 0 else -1
+        if kr <= 0 or kr != vr:
+            K, V = K.contiguous(), V.contiguous()
+    O = torch.empty(B, Hq, N, D, dtype=Q.dtype, device=device)
+    LSE = torch.empty(B, Hq, N, dtype=torch.float32, device=device) if return_lse else None
+    par, par_stride = None, 0
+    if tree_parents is not None:
+        if tree_parents.dim() == 1 and tree_parents.shape[0] == N:
+            par_stride = 0
+        elif tree_parents.dim() == 2 and tuple(tree_parents.shape) == (B, N):
+            par_stride = N
+        else:
+            tree_parents = None  # the reference falls back to the heap walk (:1470, :1475)
+        if tree_parents is not None:
+            par = tree_parents.to(device=device, dtype=torch.int32, non_blocking=True).contiguous()
+    lib = _lib.lib()
+    ws_bytes = int(lib.qattn_prefix_workspace_bytes(B, N, B * N, Hq, Hkv, D, L, int(num_splits))) if B * N else 0
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=device)
+    with torch.cuda.device(device):
+        rc = lib.qattn_ragged_tree_attn_fwd(
+            Q.data_ptr(), _lib.i64arr(Q.stride()), K.data_ptr(), _lib.i64arr(K.stride()),
+            V.data_ptr(), _lib.i64arr(V.stride()), O.data_ptr(), _lib.i64arr(O.stride()),
+            _lib.ptr(LSE), _lib.i64arr(LSE.stride()) if LSE is not None else None,
+            _lib.ptr(par), par_stride, B, N, L, Hq, Hkv, D, int(branching_factor), int(max_depth),
+            1.0 / math.sqrt(D), _dtype_code(Q), ws.data_ptr(), ws_bytes, int(num_splits), _stream(device))
+    _lib.check(rc, "qattn_ragged_tree_attn_fwd")
+    return (O, LSE) if return_lse else O
+
+
 def fused_lse_merge(
     lse_pre: torch.Tensor,
     lse_tree: torch.Tensor,

@@ -134,6 +134,40 @@ def test_abi_prefix_stride_limits():
                                            None, 0, 0, None) == -1
 
 
+def test_abi_ragged_tree_attn_validation():
+    """qattn_ragged_tree_attn_fwd over [B, H, N, D] strides: every layout it
+    cannot address is rejected before any launch; a valid layout with L = 512
+    and two forced splits stops at the missing workspace."""
+    L = _lib.lib()
+    B, H, N, P, D = 2, 4, 15, 512, 64
+    q4 = (H * N * D, N * D, D, 1)
+    k4 = (H * (P + N) * D, (P + N) * D, D, 1)
+
+    def call(qs=q4, ks=k4, vs=k4, dtype=0, head_dim=D, batch=B, num_prefix=P, par=None, par_stride=0,
+             lse=None, lss=None):
+        arr = lambda t: None if t is None else _lib.i64arr(t)
+        return L.qattn_ragged_tree_attn_fwd(FAKE, arr(qs), FAKE, arr(ks), FAKE, arr(vs), FAKE, arr(q4), lse,
+                                            arr(lss), par, par_stride, batch, N, num_prefix, H, H, head_dim,
+                                            2, 3, 0.125, dtype, None, 0, 2, None)
+
+    assert call(dtype=5) == -2
+    assert call(head_dim=96) == -3
+    assert call(qs=None) == -1
+    assert call(lse=FAKE) == -1                                       # lse without strides
+    assert call(num_prefix=-1) == -1
+    assert call(par=FAKE, par_stride=-1) == -1
+    assert call(qs=(q4[0] + 4,) + q4[1:]) == -4                       # batch stride breaks row alignment
+    assert call(ks=(k4[0] + 8,) + k4[1:]) == -4                       # not a whole number of rows
+    assert call(vs=(2 * k4[0],) + k4[1:]) == -4                       # k and v place sequences differently
+    assert call(ks=(0,) + k4[1:], vs=(0,) + k4[1:]) == -4             # sequences sharing one k/v
+    assert call(qs=q4[:3] + (2,)) == -4                               # stride_dim != 1
+    assert call() == -5
+    assert call(par=FAKE, par_stride=N, lse=FAKE, lss=(H * N, N, 1)) == -5
+    # one sequence: its batch strides are never used
+    assert call(batch=1, qs=(3,) + q4[1:], ks=(5,) + k4[1:], vs=(7,) + k4[1:]) == -5
+    assert call(batch=0) == 0
+
+
 # ---------------------------------------------------------------------------
 # Python API behaviour on the host
 # ---------------------------------------------------------------------------
@@ -153,6 +187,9 @@ def test_cpu_tensors_fail_loudly():
         ra.ragged_attention(Q, K, V, cu, 2, 2)
     with pytest.raises(RuntimeError, match="ROCm GPU"):
         ra.ragged_attention_with_parents(Q, K, V, cu, torch.zeros(7, dtype=torch.int32), 2)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        ra.ragged_tree_attn(Q.view(1, 7, 4, 64).transpose(1, 2), K.view(1, 7, 4, 64).transpose(1, 2),
+                            V.view(1, 7, 4, 64).transpose(1, 2), 2, 2)
 
 
 def test_pack_inputs():
@@ -200,6 +237,6 @@ def test_src_shim_reexports():
     import src.tree_mask as stm
     for name in ("pack_inputs", "ragged_attention", "ragged_attention_with_lse", "ragged_attention_sibling",
                  "ragged_attention_sibling_with_lse", "ragged_attention_with_parents",
-                 "ragged_attention_paged", "build_paged_kv", "fused_lse_merge"):
+                 "ragged_attention_paged", "build_paged_kv", "fused_lse_merge", "ragged_tree_attn"):
         assert getattr(sra, name) is getattr(ra, name)
     assert stm.tree_attention_mask is tm.tree_attention_mask
