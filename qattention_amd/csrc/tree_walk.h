@@ -194,6 +194,7 @@ struct Walk4 {
     const int64_t kvb;
     const uint16_t* kb;
     const uint16_t* vb;
+    const int32_t tok0;  // the query's own node: the row a step without a key reads
     int32_t cur, prev;
     int s0;
     bool val[CH];
@@ -203,42 +204,66 @@ struct Walk4 {
                                      int j)
         : p(p_), seq(seq_), pb(parents_base<BATCH>(p_, seq_, start_)), n(n_), kvb(kv_base(p_, seq_, start_)),
           kb((const uint16_t*)p_.k + (int64_t)kvh * p_.sk_h + 8 * j),
-          vb((const uint16_t*)p_.v + (int64_t)kvh * p_.sv_h + 8 * j), cur(tok), prev(-1), s0(0) {}
+          vb((const uint16_t*)p_.v + (int64_t)kvh * p_.sv_h + 8 * j), tok0(tok), cur(tok), prev(-1), s0(0) {}
 
-    // Issue the K/V loads of steps s0 .. s0 + CH - 1.
+    // Issue the K/V loads of steps s0 .. s0 + CH - 1.  A parents walk asks
+    // for each step's next node before that step's K/V rows: loads complete
+    // in order, so waiting for the parent leaves the K/V loads in flight, and
+    // a chunk costs two round trips rather than one per step plus one.
+    // Packed K/V loads are unconditional: a step without a key (past
+    // max_depth, or a stalled walk) reads the query's own row, which is in
+    // bounds and already attended, and fold gives it score -inf (weight 0).
+    // A guarded load would let the compiler move the fold's conversions
+    // behind each load and wait for it there, one round trip per row.
     __device__ __forceinline__ void issue() {
-        int64_t ko[CH], vo[CH];
 #pragma unroll
         for (int t = 0; t < CH; ++t) {
             bool ok = (s0 + t <= p.max_depth) && (cur != prev);
+            int32_t par = 0;
+            if constexpr (WALK == WALK_PARENTS) par = p.parents[pb + cur];  // src/ragged_attn.py:692-694
+            int64_t ko, vo;
             if constexpr (LAYOUT == KV_PACKED) {
-                ko[t] = (kvb + cur) * p.sk_t;
-                vo[t] = (kvb + cur) * p.sv_t;
+                ko = (kvb + cur) * p.sk_t;
+                vo = (kvb + cur) * p.sv_t;
             } else {
                 const int32_t lp = cur / p.page_size;
                 const int32_t sl = cur - lp * p.page_size;
                 int32_t pg = -1;
                 if (ok && lp < p.pt_cols) pg = p.page_table[(int64_t)seq * p.pt_cols + lp];
                 ok = ok && pg >= 0 && pg < p.num_pages;
-                ko[t] = (int64_t)pg * p.sk_page + (int64_t)sl * p.sk_t;
-                vo[t] = (int64_t)pg * p.sv_page + (int64_t)sl * p.sv_t;
+                ko = (int64_t)pg * p.sk_page + (int64_t)sl * p.sk_t;
+                vo = (int64_t)pg * p.sv_page + (int64_t)sl * p.sv_t;
             }
             val[t] = ok;
-            prev = cur;
-            cur = walk_next<WALK>(p, pb, n, cur);
-        }
+            if constexpr (LAYOUT == KV_PACKED) {
+                if (!ok) {
+                    ko = (kvb + tok0) * p.sk_t;
+                    vo = (kvb + tok0) * p.sv_t;
+                }
 #pragma unroll
-        for (int t = 0; t < CH; ++t) {
+                for (int i = 0; i < NCH; ++i) {
+                    kf[t][i] = ld16(kb + ko + 32 * i);
+                    vf[t][i] = ld16(vb + vo + 32 * i);
+                }
+            } else {
 #pragma unroll
-            for (int i = 0; i < NCH; ++i) {
-                kf[t][i] = Vec16{{0u, 0u, 0u, 0u}};
-                vf[t][i] = Vec16{{0u, 0u, 0u, 0u}};
-                if (val[t]) {
-                    kf[t][i] = ld16(kb + ko[t] + 32 * i);
-                    vf[t][i] = ld16(vb + vo[t] + 32 * i);
+                for (int i = 0; i < NCH; ++i) {
+                    kf[t][i] = Vec16{{0u, 0u, 0u, 0u}};
+                    vf[t][i] = Vec16{{0u, 0u, 0u, 0u}};
+                    if (ok) {
+                        kf[t][i] = ld16(kb + ko + 32 * i);
+                        vf[t][i] = ld16(vb + vo + 32 * i);
+                    }
                 }
             }
+            prev = cur;
+            if constexpr (WALK == WALK_PARENTS)
+                cur = (par >= 0 && par < n) ? par : cur;
+            else
+                cur = walk_next<WALK>(p, pb, n, cur);
         }
+        // keep the fold's arithmetic below the chunk's loads
+        __builtin_amdgcn_sched_barrier(0);
     }
 
     // Fold the issued chunk into (m, l, acc) and move to the next chunk.
