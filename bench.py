@@ -1,6 +1,6 @@
 """Benchmark of the tree-verify attention hot path on one MI355X.
 
-    python bench.py [--steps K] [--warmup W] [--config cfg2|cfg3|cfg4|cfg5|gen1024|cfg4_bhnd] [--algo auto|gather|subtree]
+    python bench.py [--steps K] [--warmup W] [--config cfg2|cfg3|cfg4|cfg5|gen1024|cfg4_bhnd|cfg2_paged] [--algo auto|gather|subtree]
 
 A step is one full verify-attention call (all sequences, all heads, and the
 prefix KV cache when the config has one) over one batch of synthetic input,
@@ -55,6 +55,9 @@ CONFIGS = {
     # cfg4 as the reference's E2E verify step holds it (scripts/e2e_benchmark.py:
     # 1394-1502): Q [B, H, N, D], K/V [B, Hkv, L + N, D], one ragged_tree_attn call
     "cfg4_bhnd": dict(B=4, b=4, d=3, H=32, Hkv=8, D=128, L=10240, sigma=1.0, layout="bhnd"),
+    # cfg2 with K/V in a paged cache of 16-token pages (the reference's page
+    # size, src/ragged_attn.py:945) placed in a shuffled physical order
+    "cfg2_paged": dict(B=4, b=4, d=5, H=32, Hkv=32, D=128, L=0, sigma=1.0, layout="paged"),
 }
 
 
@@ -227,6 +230,7 @@ def main():
 
     seed = B * 10000 + b * 100 + d
     bhnd = c.get("layout") == "bhnd"
+    paged = c.get("layout") == "paged"
     sets = []
     for i in range(nsets):
         Q, K, V, Kp, Vp = make_set(c, seed + i, torch.float16)
@@ -236,6 +240,12 @@ def main():
             K = torch.cat([Kp, K.view(B, N, Hkv, D)], 1).permute(0, 2, 1, 3).contiguous()
             V = torch.cat([Vp, V.view(B, N, Hkv, D)], 1).permute(0, 2, 1, 3).contiguous()
             Kp = Vp = None
+        if paged:
+            Kc, Vc, pt = ra.build_paged_kv(list(K.view(B, N, Hkv, D)), list(V.view(B, N, Hkv, D)), 16)
+            perm = torch.randperm(Kc.shape[0], generator=torch.Generator().manual_seed(seed + i))
+            K, V = torch.empty_like(Kc), torch.empty_like(Vc)
+            K[perm], V[perm] = Kc, Vc
+            Kp = perm.to(torch.int32)[pt.long()]  # the page table rides in the prefix slot
         sets.append([t.to(dev) if t is not None else None for t in (Q, K, V, Kp, Vp)])
     cu = torch.arange(0, (B + 1) * N, N, dtype=torch.int32, device=dev)
     parents = torch.tensor(heap_parents(b, N) * B, dtype=torch.int32, device=dev) if parents_walk else None
@@ -245,6 +255,8 @@ def main():
         Q, K, V, Kp, Vp = sets[i]
         if bhnd:
             return ra.ragged_tree_attn(Q, K, V, b, d)
+        if paged:
+            return ra.ragged_attention_paged(Q, K, V, Kp, cu, b, d, max_seqlen=N)
         if L:
             return ra.ragged_attention_prefix(Q, K, V, cu, Kp, Vp, b, d, max_seqlen=N)
         if parents_walk:
@@ -334,7 +346,8 @@ def main():
         "data": f"synthetic N(0,{c['sigma']}^2), CPU-seeded (seed B*10000+b*100+d), {nsets} rotating sets",
         "config": {"workload": f"{args.config}: verify attention B={B} b={b} d={d} N={N} H={H} Hkv={Hkv} "
                                f"D={D} L={L} fp16" + (", explicit parents" if parents_walk else "")
-                               + (", [B, H, N, D] views" if bhnd else ""), "B": B, "b": b, "d": d, "N": N, "H": H, "Hkv": Hkv,
+                               + (", [B, H, N, D] views" if bhnd else "")
+                               + (", paged K/V (16-token pages, shuffled)" if paged else ""), "B": B, "b": b, "d": d, "N": N, "H": H, "Hkv": Hkv,
                    "D": D, "L": L, "tokens": T, "algo": args.algo},
         "achieved_GBps": round(achieved_bw / 1e9, 1),
         "wall_us_per_call": round(wall_us, 2),

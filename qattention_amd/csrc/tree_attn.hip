@@ -71,7 +71,11 @@ __global__ __launch_bounds__(kThreads) void tree_gather_kernel(TreeParams p) {
     float m = -INFINITY, l = 0.f, acc[8 * NCH];
     // the first chunk of the walk's K/V loads is in flight while the prefix
     // splits are merged (the walk does not depend on them)
-    Walk4<T, D, WALK, LAYOUT, 8 / (D / 32), BATCH> w(p, seq, start, n, tok, h / p.group, j);
+    // (a paged step without a valid page reads this query's own Q row)
+    const uint16_t* qdummy = (const uint16_t*)p.q + qrow * p.sq_t + (BATCH ? (int64_t)seq * p.sq_b : 0) +
+                             (int64_t)h * p.sq_h + 8 * j;
+    Walk4<T, D, WALK, LAYOUT, 8 / (D / 32), BATCH> w(p, seq, start, n, tok, h / p.group, j,
+                                                     LAYOUT == KV_PAGED ? qdummy : nullptr);
     w.issue();
     if constexpr (PSTATE) {
         load_partial_state4<D>(p, qrow, h, j, m, l, acc);

@@ -195,26 +195,30 @@ struct Walk4 {
     const uint16_t* kb;
     const uint16_t* vb;
     const int32_t tok0;  // the query's own node: the row a step without a key reads
+    const uint16_t* qdummy;  // paged: the query's Q row chunk, read by a step without a valid page
     int32_t cur, prev;
     int s0;
     bool val[CH];
     Vec16 kf[CH][NCH], vf[CH][NCH];
 
     __device__ __forceinline__ Walk4(const TreeParams& p_, int seq_, int32_t start_, int32_t n_, int tok, int kvh,
-                                     int j)
+                                     int j, const uint16_t* qdummy_ = nullptr)
         : p(p_), seq(seq_), pb(parents_base<BATCH>(p_, seq_, start_)), n(n_), kvb(kv_base(p_, seq_, start_)),
           kb((const uint16_t*)p_.k + (int64_t)kvh * p_.sk_h + 8 * j),
-          vb((const uint16_t*)p_.v + (int64_t)kvh * p_.sv_h + 8 * j), tok0(tok), cur(tok), prev(-1), s0(0) {}
+          vb((const uint16_t*)p_.v + (int64_t)kvh * p_.sv_h + 8 * j), tok0(tok), qdummy(qdummy_), cur(tok),
+          prev(-1), s0(0) {}
 
     // Issue the K/V loads of steps s0 .. s0 + CH - 1.  A parents walk asks
     // for each step's next node before that step's K/V rows: loads complete
     // in order, so waiting for the parent leaves the K/V loads in flight, and
     // a chunk costs two round trips rather than one per step plus one.
-    // Packed K/V loads are unconditional: a step without a key (past
-    // max_depth, or a stalled walk) reads the query's own row, which is in
-    // bounds and already attended, and fold gives it score -inf (weight 0).
-    // A guarded load would let the compiler move the fold's conversions
-    // behind each load and wait for it there, one round trip per row.
+    // K/V loads are unconditional: a step without a key (past max_depth, a
+    // stalled walk) reads the query's own row (packed: in bounds and already
+    // attended), or for a paged step without a valid page the query's Q row
+    // (in bounds; finite whenever the output can be), and fold gives it score
+    // -inf (weight 0).  A guarded load would let the compiler move the fold's
+    // conversions behind each load and wait for it there, one round trip per
+    // row.
     __device__ __forceinline__ void issue() {
 #pragma unroll
         for (int t = 0; t < CH; ++t) {
@@ -235,26 +239,23 @@ struct Walk4 {
                 vo = (int64_t)pg * p.sv_page + (int64_t)sl * p.sv_t;
             }
             val[t] = ok;
+            const uint16_t* kr;
+            const uint16_t* vr;
             if constexpr (LAYOUT == KV_PACKED) {
                 if (!ok) {
                     ko = (kvb + tok0) * p.sk_t;
                     vo = (kvb + tok0) * p.sv_t;
                 }
-#pragma unroll
-                for (int i = 0; i < NCH; ++i) {
-                    kf[t][i] = ld16(kb + ko + 32 * i);
-                    vf[t][i] = ld16(vb + vo + 32 * i);
-                }
+                kr = kb + ko;
+                vr = vb + vo;
             } else {
+                kr = ok ? kb + ko : qdummy;
+                vr = ok ? vb + vo : qdummy;
+            }
 #pragma unroll
-                for (int i = 0; i < NCH; ++i) {
-                    kf[t][i] = Vec16{{0u, 0u, 0u, 0u}};
-                    vf[t][i] = Vec16{{0u, 0u, 0u, 0u}};
-                    if (ok) {
-                        kf[t][i] = ld16(kb + ko + 32 * i);
-                        vf[t][i] = ld16(vb + vo + 32 * i);
-                    }
-                }
+            for (int i = 0; i < NCH; ++i) {
+                kf[t][i] = ld16(kr + 32 * i);
+                vf[t][i] = ld16(vr + 32 * i);
             }
             prev = cur;
             if constexpr (WALK == WALK_PARENTS)

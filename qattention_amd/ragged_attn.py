@@ -262,9 +262,12 @@ def ragged_attention_paged(
     cu_seqlens: torch.Tensor,
     branching_factor: int,
     max_depth: int,
+    max_seqlen: int = None,
 ) -> torch.Tensor:
     """Ancestor-sparse attention reading K/V from a paged cache
-    (src/ragged_attn.py:932-1003).
+    (src/ragged_attn.py:932-1003).  max_seqlen (not in the reference, which
+    always reads cu_seqlens on the host) skips that read, as in
+    ragged_attention, so the call can be captured in a graph.
 
     K_cache/V_cache: [pages, PAGE_SIZE, Hkv, D]; page_table: [B, max_pages]
     int32 logical->physical page map; ancestor position c of sequence b is
@@ -277,7 +280,7 @@ def ragged_attention_paged(
     if Dk != D or Hkv < 1 or Hq % Hkv != 0:
         raise ValueError(f"cache shape {tuple(K_cache.shape)} incompatible with Q {tuple(Q.shape)}")
     B = int(cu_seqlens.shape[0]) - 1
-    ms, cu_dev = _seqlens(cu_seqlens, B, device, None)  # the reference always reads cu on host
+    ms, cu_dev = _seqlens(cu_seqlens, B, device, max_seqlen)
     pt = page_table.to(device=device, dtype=torch.int32, non_blocking=True).contiguous()
     if pt.dim() != 2 or pt.shape[0] < B:
         raise ValueError(f"page_table must be [B, max_pages] (got {tuple(page_table.shape)})")

@@ -395,6 +395,39 @@ def test_paged(page_size):
     check_fp16(O.double().cpu().numpy(), o_ref, "paged")
 
 
+def test_paged_missing_pages():
+    """Page-table entries that are negative or past num_pages skip the
+    ancestors on those pages (qattn.h); a query whose own page and every
+    ancestor's page are missing attends nothing and gets O = 0.  The oracle
+    is the heap walk's ancestor table with those entries removed."""
+    ra, _ = _ra()
+    ps, b, d = 4, 3, 3
+    lens = [40, 17]
+    Q, K, V, cu = make_inputs(lens, 4, 64, 2031, Hkv=2)
+    cuL = cu.tolist()
+    ks = [K[cuL[i]:cuL[i + 1]].to(DEV) for i in range(2)]
+    vs = [V[cuL[i]:cuL[i + 1]].to(DEV) for i in range(2)]
+    Kc, Vc, pt = ra.build_paged_kv(ks, vs, page_size=ps)
+    pt = pt.clone()
+    pt[0, 0] = -1                 # sequence 0's root page: tokens 0..3 and every root step
+    pt[0, 5] = Kc.shape[0] + 5    # past num_pages
+    pt[1, 2] = -7
+    anc = clib.ancestor_table_heap(cu.numpy().astype(np.int32), b, d)
+    for t in range(anc.shape[0]):
+        seq = 0 if t < cuL[1] else 1
+        for s1 in range(anc.shape[1]):
+            a = anc[t, s1]
+            if a >= 0:
+                page = int(pt[seq, a // ps])
+                if page < 0 or page >= Kc.shape[0]:
+                    anc[t, s1] = -1
+    assert (anc[:cuL[1]] < 0).all(axis=1).any()  # some query attends nothing
+    o_ref, _ = clib.tree_attn(Q.float().numpy(), K.float().numpy(), V.float().numpy(), cu.numpy(), anc,
+                              1.0 / 8.0)
+    O = ra.ragged_attention_paged(Q.to(DEV), Kc, Vc, pt, cu, b, d)
+    check_fp16(O.double().cpu().numpy(), o_ref, "paged, missing pages")
+
+
 # ---------------------------------------------------------------------------
 # LSE merge
 # ---------------------------------------------------------------------------
