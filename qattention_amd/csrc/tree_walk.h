@@ -220,38 +220,19 @@ struct Walk4 {
     // conversions behind each load and wait for it there, one round trip per
     // row.
     __device__ __forceinline__ void issue() {
+        if constexpr (LAYOUT == KV_PAGED) {
+            issue_paged();
+            return;
+        }
 #pragma unroll
         for (int t = 0; t < CH; ++t) {
             bool ok = (s0 + t <= p.max_depth) && (cur != prev);
             int32_t par = 0;
             if constexpr (WALK == WALK_PARENTS) par = p.parents[pb + cur];  // src/ragged_attn.py:692-694
-            int64_t ko, vo;
-            if constexpr (LAYOUT == KV_PACKED) {
-                ko = (kvb + cur) * p.sk_t;
-                vo = (kvb + cur) * p.sv_t;
-            } else {
-                const int32_t lp = cur / p.page_size;
-                const int32_t sl = cur - lp * p.page_size;
-                int32_t pg = -1;
-                if (ok && lp < p.pt_cols) pg = p.page_table[(int64_t)seq * p.pt_cols + lp];
-                ok = ok && pg >= 0 && pg < p.num_pages;
-                ko = (int64_t)pg * p.sk_page + (int64_t)sl * p.sk_t;
-                vo = (int64_t)pg * p.sv_page + (int64_t)sl * p.sv_t;
-            }
             val[t] = ok;
-            const uint16_t* kr;
-            const uint16_t* vr;
-            if constexpr (LAYOUT == KV_PACKED) {
-                if (!ok) {
-                    ko = (kvb + tok0) * p.sk_t;
-                    vo = (kvb + tok0) * p.sv_t;
-                }
-                kr = kb + ko;
-                vr = vb + vo;
-            } else {
-                kr = ok ? kb + ko : qdummy;
-                vr = ok ? vb + vo : qdummy;
-            }
+            const int32_t row = ok ? cur : tok0;
+            const uint16_t* kr = kb + (kvb + row) * p.sk_t;
+            const uint16_t* vr = vb + (kvb + row) * p.sv_t;
 #pragma unroll
             for (int i = 0; i < NCH; ++i) {
                 kf[t][i] = ld16(kr + 32 * i);
@@ -264,6 +245,44 @@ struct Walk4 {
                 cur = walk_next<WALK>(p, pb, n, cur);
         }
         // keep the fold's arithmetic below the chunk's loads
+        __builtin_amdgcn_sched_barrier(0);
+    }
+
+    // Paged K/V (heap walk): the chunk's nodes are arithmetic, so every
+    // step's page-table entry is requested before any K/V row and the wait
+    // for them leaves no row load behind it (two round trips per chunk).  The
+    // entry loads are unconditional too: a logical page past pt_cols reads
+    // the row's last entry (or, for an empty table, the Q row) and is
+    // discarded.
+    __device__ __forceinline__ void issue_paged() {
+        int32_t pg[CH], sl[CH];
+        bool okn[CH];
+#pragma unroll
+        for (int t = 0; t < CH; ++t) {
+            okn[t] = (s0 + t <= p.max_depth) && (cur != prev);
+            const int32_t lp = cur / p.page_size;
+            sl[t] = cur - lp * p.page_size;
+            okn[t] = okn[t] && lp < p.pt_cols;
+            const int32_t* ent = p.pt_cols > 0
+                                     ? p.page_table + (int64_t)seq * p.pt_cols + min(lp, p.pt_cols - 1)
+                                     : (const int32_t*)qdummy;
+            pg[t] = *ent;
+            prev = cur;
+            cur = walk_next<WALK>(p, pb, n, cur);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int t = 0; t < CH; ++t) {
+            const bool ok = okn[t] && pg[t] >= 0 && pg[t] < p.num_pages;
+            val[t] = ok;
+            const uint16_t* kr = ok ? kb + (int64_t)pg[t] * p.sk_page + (int64_t)sl[t] * p.sk_t : qdummy;
+            const uint16_t* vr = ok ? vb + (int64_t)pg[t] * p.sv_page + (int64_t)sl[t] * p.sv_t : qdummy;
+#pragma unroll
+            for (int i = 0; i < NCH; ++i) {
+                kf[t][i] = ld16(kr + 32 * i);
+                vf[t][i] = ld16(vr + 32 * i);
+            }
+        }
         __builtin_amdgcn_sched_barrier(0);
     }
 
