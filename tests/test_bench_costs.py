@@ -1,0 +1,66 @@
+"""Host checks of bench.py: the algorithmic bytes and FLOPs every roofline
+figure is computed from, against independent arithmetic for each config
+(compulsory Q+K+V+O bytes at the head counts; FLOPs from the mean ancestor
+chain of the heap walk), and the single-GPU contract."""
+from __future__ import annotations
+
+import os
+import subprocess
+import sys
+
+import pytest
+
+from conftest import ROOT
+
+sys.path.insert(0, ROOT)
+import bench  # noqa: E402
+
+
+def _chain_sum(b, d, n):
+    """Attended (query, key) pairs of one heap-indexed sequence of n nodes:
+    every node attends itself and its ancestors up to d steps."""
+    total = 0
+    for i in range(n):
+        depth, x = 0, i
+        while x > 0:
+            x = (x - 1) // b
+            depth += 1
+        total += min(depth, d) + 1
+    return total
+
+
+@pytest.mark.parametrize("name,bytes_,mean_chain", [
+    ("cfg2", 178_913_280, 5.668),   # 4 * T*H*D*2 with T = 5460, H = 32, D = 128
+    ("cfg3", 268_173_312, 9.010),   # T = 8184
+    ("gen1024", 33_554_432, None),  # B = 1, N = 1024
+])
+def test_tree_configs(name, bytes_, mean_chain):
+    c = bench.CONFIGS[name]
+    alg_bytes, flops, prefix_flops = bench.model_costs(c)
+    assert alg_bytes == bytes_ and prefix_flops == 0
+    N = bench.tree_size(c)
+    pairs = _chain_sum(c["b"], c["d"], N)
+    assert flops == 4 * c["D"] * c["H"] * c["B"] * pairs
+    if mean_chain is not None:
+        assert abs(pairs / N - mean_chain) < 5e-4
+
+
+def test_prefix_configs():
+    # cfg4: GQA-native bytes (prefix K/V at Hkv = 8) and the prefix FLOPs
+    alg_bytes, flops, prefix_flops = bench.model_costs(bench.CONFIGS["cfg4"])
+    assert alg_bytes == 174_735_360
+    assert prefix_flops == 4 * 4 * 85 * 32 * 10240 * 128 == 57_042_534_400
+    assert flops - prefix_flops == 4 * 128 * 32 * 4 * _chain_sum(4, 3, 85)
+    # cfg5: tree Q+K+V+O 2454.2 MB + prefix K/V 536.9 MB
+    alg_bytes, flops, prefix_flops = bench.model_costs(bench.CONFIGS["cfg5"])
+    assert alg_bytes == 2_454_192_128 + 536_870_912
+    assert prefix_flops == 4 * 16 * 4681 * 32 * 2048 * 128
+    # the same workload in other layouts costs the same
+    assert bench.model_costs(bench.CONFIGS["cfg4_bhnd"]) == bench.model_costs(bench.CONFIGS["cfg4"])
+    assert bench.model_costs(bench.CONFIGS["cfg2_paged"]) == bench.model_costs(bench.CONFIGS["cfg2"])
+
+
+def test_more_than_one_gpu_is_refused():
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 2 and "one GPU" in r.stdout + r.stderr
