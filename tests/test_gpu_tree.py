@@ -428,6 +428,36 @@ def test_paged_missing_pages():
     check_fp16(O.double().cpu().numpy(), o_ref, "paged, missing pages")
 
 
+def test_paged_graph_capture_replay():
+    """With max_seqlen (and device cu / page table) the paged call makes no
+    host read and records into a HIP graph; replays after new cache contents
+    are copied in match eager calls on the same contents."""
+    ra, _ = _ra()
+    b, d, N, B, ps = 3, 4, 121, 3, 16
+    Q, K, V, cu = make_inputs([N] * B, 8, 128, 2040, Hkv=4)
+    Kc, Vc, pt = ra.build_paged_kv(list(K.to(DEV).view(B, N, 4, 128)), list(V.to(DEV).view(B, N, 4, 128)), ps)
+    Qd, cud, ptd = Q.to(DEV), cu.to(DEV), pt.to(DEV)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        ra.ragged_attention_paged(Qd, Kc, Vc, ptd, cud, b, d, max_seqlen=N)
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = ra.ragged_attention_paged(Qd, Kc, Vc, ptd, cud, b, d, max_seqlen=N)
+    g = torch.Generator().manual_seed(2041)
+    for i in range(3):
+        Kc.copy_(torch.randn(Kc.shape, generator=g).half())
+        Vc.copy_(torch.randn(Vc.shape, generator=g).half())
+        Qd.copy_(torch.randn(Qd.shape, generator=g).half())
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        eager = ra.ragged_attention_paged(Qd, Kc, Vc, ptd, cud, b, d, max_seqlen=N)
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {i}"
+
+
 # ---------------------------------------------------------------------------
 # LSE merge
 # ---------------------------------------------------------------------------
