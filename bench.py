@@ -1,6 +1,6 @@
 """Benchmark of the tree-verify attention hot path on one MI355X.
 
-    python bench.py [--steps K] [--warmup W] [--config cfg2|cfg3|cfg4|cfg5|gen1024|cfg4_bhnd|cfg2_paged] [--algo auto|gather|subtree]
+    python bench.py [--steps K] [--warmup W] [--config cfg2|cfg3|cfg4|cfg5|gen1024|cfg4_bhnd|cfg2_paged|eagle3] [--algo auto|gather|subtree]
 
 A step is one full verify-attention call (all sequences, all heads, and the
 prefix KV cache when the config has one) over one batch of synthetic input,
@@ -58,6 +58,12 @@ CONFIGS = {
     # cfg2 with K/V in a paged cache of 16-token pages (the reference's page
     # size, src/ragged_attn.py:945) placed in a shuffled physical order
     "cfg2_paged": dict(B=4, b=4, d=5, H=32, Hkv=32, D=128, L=0, sigma=1.0, layout="paged"),
+    # one EAGLE-3 verify step of Llama-3.1-8B as the reference's E2E harness
+    # runs it (scripts/e2e_benchmark.py:741-744, 875: total_token 60, depth 7,
+    # top_k 10; B = 1) over a 2048-token KV cache: [B, H, N, D] tensors, the
+    # draft tree as a parent array, one ragged_tree_attn call
+    "eagle3": dict(B=1, b=10, d=7, H=32, Hkv=8, D=128, L=2048, sigma=1.0, N=60, walk="eagle",
+                   layout="bhnd"),
 }
 
 
@@ -73,6 +79,25 @@ def tree_size(c):
 def heap_parents(b, n):
     """Sequence-local parent array of a heap-indexed tree, the root its own parent."""
     return [0] + [(i - 1) // b for i in range(1, n)]
+
+
+def eagle_parents(n, depth):
+    """A draft tree of n nodes in BFS order, depth levels below the root,
+    levels as even as n allows; node j of a level hangs under node j mod
+    (previous level size) of the level above.  The root is its own parent."""
+    sizes = [1] + [(n - 1) // depth + (1 if i < (n - 1) % depth else 0) for i in range(depth)]
+    par, first = [0], 0
+    for lv in range(1, len(sizes)):
+        prev = sizes[lv - 1]
+        par += [first + j % prev for j in range(sizes[lv])]
+        first += prev
+    return par
+
+
+def tree_parents(c):
+    """Parent array of one sequence of the config's tree."""
+    n = tree_size(c)
+    return eagle_parents(n, c["d"]) if c.get("walk") == "eagle" else heap_parents(c["b"], n)
 
 
 def make_set(c, seed, dtype):
@@ -100,9 +125,10 @@ def model_costs(c):
     tree_bytes = 2 * T * D * (2 * H + 2 * Hkv)          # Q + O at H, tree K + V at Hkv
     prefix_bytes = 2 * 2 * B * L * Hkv * D                 # prefix K + V at Hkv
     # attended (query, key) pairs per sequence: min(depth, d) + 1 per node
+    par = tree_parents(c)
     depth = [0] * N
     for i in range(1, N):
-        depth[i] = depth[(i - 1) // b] + 1 if b > 1 else i
+        depth[i] = depth[par[i]] + 1 if (b > 1 or c.get("walk") == "eagle") else i
     steps = sum(min(x, d) + 1 for x in depth)
     tree_flops = 4 * D * H * B * steps
     prefix_flops = 4 * B * N * H * L * D
@@ -157,7 +183,16 @@ def cpu_baseline(c, budget_s=20.0):
     Kp = Kp[:nseq].float() if Kp is not None else None
     Vp = Vp[:nseq].float() if Vp is not None else None
     cu = torch.arange(0, (nseq + 1) * N, N, dtype=torch.int32)
-    masks = [tree.tree_attention_mask_n(b, N)] * nseq
+    if c.get("walk") in ("parents", "eagle"):
+        # the walk's tree: every node attends its ancestors (the root holds -1 here)
+        pa = [-1] + tree_parents(c)[1:]
+        m = np.zeros((N, N), dtype=bool)
+        for i in range(N):
+            for a in tree.ancestors(i, pa):
+                m[i, a] = True
+        masks = [m] * nseq
+    else:
+        masks = [tree.tree_attention_mask_n(b, N)] * nseq
 
     def run():
         sdpa.packed_tree_attention(Q, K, V, cu, masks, Kp=Kp, Vp=Vp)
@@ -221,7 +256,7 @@ def main():
     B, b, d, H, Hkv, D, L = (c[k] for k in ("B", "b", "d", "H", "Hkv", "D", "L"))
     N = tree_size(c)
     T = B * N
-    parents_walk = c.get("walk") == "parents"
+    parents_walk = c.get("walk") in ("parents", "eagle")
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     algo = {"auto": _lib.ALGO_AUTO, "gather": _lib.ALGO_GATHER, "subtree": _lib.ALGO_SUBTREE}[args.algo]
@@ -248,13 +283,13 @@ def main():
             Kp = perm.to(torch.int32)[pt.long()]  # the page table rides in the prefix slot
         sets.append([t.to(dev) if t is not None else None for t in (Q, K, V, Kp, Vp)])
     cu = torch.arange(0, (B + 1) * N, N, dtype=torch.int32, device=dev)
-    parents = torch.tensor(heap_parents(b, N) * B, dtype=torch.int32, device=dev) if parents_walk else None
+    parents = torch.tensor(tree_parents(c) * B, dtype=torch.int32, device=dev) if parents_walk else None
     torch.cuda.synchronize()
 
     def call(i):
         Q, K, V, Kp, Vp = sets[i]
         if bhnd:
-            return ra.ragged_tree_attn(Q, K, V, b, d)
+            return ra.ragged_tree_attn(Q, K, V, b, d, parents[:N] if parents_walk else None)
         if paged:
             return ra.ragged_attention_paged(Q, K, V, Kp, cu, b, d, max_seqlen=N)
         if L:

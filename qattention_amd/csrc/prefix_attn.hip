@@ -247,13 +247,16 @@ __global__ __launch_bounds__(kPrefixThreads) __attribute__((amdgpu_waves_per_eu(
     // into the exponent: p = exp2(s c - m c), one FMA.  Lazy rescaling: the
     // exponent reference m_run only moves when a block max exceeds it by more
     // than kLazy/c (a factor 2^kLazy in P), so the accumulators are rescaled on
-    // a handful of blocks.  P stays <= 2^kLazy (exact in fp16/bf16 range, same
-    // relative precision) and l carries the same reference.
+    // a handful of blocks.  P stays <= 2^kLazy and l carries the same
+    // reference.  The PV product rounds P to the input type while l sums it
+    // unrounded, so the largest weight is exact only when it is 1: bf16 (8
+    // mantissa bits) therefore moves the reference on every new maximum, as
+    // the reference's FA2 loop does; fp16 (11 bits) keeps the lazy reference.
     const float csc = p.scale_log2;
     auto softmax = [&](f4_t (&s)[kQB][4], Vec16 (&pf)[kQB][2], float (&alpha)[kQB], bool& rescale, int kb,
                        auto mask_tag) {
         constexpr bool MASK = decltype(mask_tag)::value;
-        constexpr float kLazy = 8.f;
+        constexpr float kLazy = T::kCode == QATTN_DTYPE_BF16 ? 0.f : 8.f;
         if constexpr (MASK) {  // tail block of the split: keys at or beyond k_hi do not exist
 #pragma unroll
             for (int b = 0; b < kQB; ++b)
@@ -601,7 +604,15 @@ static int64_t units_per_split(int batch, int hkv, int max_seqlen, int group) {
 static int prefix_splits(int64_t ups, int L, int num_splits, int& blocks_per_split) {
     const int blocks = (L + kBN - 1) / kBN;
     int s = num_splits;
-    if (s <= 0) s = (int)std::max<int64_t>(1, (512 + ups / 2) / ups);
+    if (s <= 0) {
+        s = (int)std::max<int64_t>(1, (512 + ups / 2) / ups);
+        // Every split writes a partial state that the merge reads back; with
+        // few query rows (one decode step of a small tree) that traffic and the
+        // per-split overheads outgrow the split's own work.  Keep at least a
+        // quarter of the blocks, within 2..8, per split.
+        const int bps_min = std::min(8, std::max(2, blocks / 4));
+        s = std::min(s, std::max(1, blocks / bps_min));
+    }
     s = std::max(1, std::min(s, std::max(blocks, 1)));
     blocks_per_split = (blocks + s - 1) / s;
     return blocks_per_split > 0 ? (blocks + blocks_per_split - 1) / blocks_per_split : 1;
