@@ -55,6 +55,18 @@ def test_prefix_configs():
     alg_bytes, flops, prefix_flops = bench.model_costs(bench.CONFIGS["cfg5"])
     assert alg_bytes == 2_454_192_128 + 536_870_912
     assert prefix_flops == 4 * 16 * 4681 * 32 * 2048 * 128
+    # eagle3: a 60-node draft tree of depth 7 (levels as even as 59 nodes
+    # allow: 9, 9, 9, 8, 8, 8, 8) over a 2048-token cache at Hkv = 8
+    par = bench.eagle_parents(60, 7)
+    depth = [0] * 60
+    for i in range(1, 60):
+        assert par[i] < i
+        depth[i] = depth[par[i]] + 1
+    assert max(depth) == 7 and [depth.count(k) for k in range(8)] == [1, 9, 9, 9, 8, 8, 8, 8]
+    alg_bytes, flops, prefix_flops = bench.model_costs(bench.CONFIGS["eagle3"])
+    assert alg_bytes == 2 * 60 * 128 * (2 * 32 + 2 * 8) + 2 * 2 * 2048 * 8 * 128 == 9_617_408
+    assert prefix_flops == 4 * 60 * 32 * 2048 * 128
+    assert flops - prefix_flops == 4 * 128 * 32 * sum(x + 1 for x in depth)
     # the same workload in other layouts costs the same
     assert bench.model_costs(bench.CONFIGS["cfg4_bhnd"]) == bench.model_costs(bench.CONFIGS["cfg4"])
     assert bench.model_costs(bench.CONFIGS["cfg2_paged"]) == bench.model_costs(bench.CONFIGS["cfg2"])
