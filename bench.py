@@ -1,6 +1,6 @@
 """Benchmark of the tree-verify attention hot path on one MI355X.
 
-    python bench.py [--steps K] [--warmup W] [--config cfg2|cfg3|cfg4|cfg5|gen1024|cfg4_bhnd|cfg2_paged|eagle3] [--algo auto|gather|subtree]
+    python bench.py [--steps K] [--warmup W] [--config cfg2|cfg3|cfg4|cfg5|gen1024|cfg4_bhnd|cfg2_paged|eagle3|merge4] [--algo auto|gather|subtree]
 
 A step is one full verify-attention call (all sequences, all heads, and the
 prefix KV cache when the config has one) over one batch of synthetic input,
@@ -64,6 +64,9 @@ CONFIGS = {
     # draft tree as a parent array, one ragged_tree_attn call
     "eagle3": dict(B=1, b=10, d=7, H=32, Hkv=8, D=128, L=2048, sigma=1.0, N=60, walk="eagle",
                    layout="bhnd"),
+    # fused_lse_merge (src/ragged_attn.py:1619-1653) at cfg4's verify shape:
+    # two [B, H, Nq, D] blocks and their LSEs merged into one output
+    "merge4": dict(B=4, b=4, d=3, H=32, Hkv=32, D=128, L=0, sigma=1.0, layout="merge"),
 }
 
 
@@ -122,6 +125,9 @@ def model_costs(c):
     B, b, d, H, Hkv, D, L = (c[k] for k in ("B", "b", "d", "H", "Hkv", "D", "L"))
     N = tree_size(c)
     T = B * N
+    if c.get("layout") == "merge":
+        # read two O blocks and two fp32 LSEs, write one O; ~6 FLOP per element
+        return 3 * 2 * T * H * D + 2 * 4 * T * H, 6 * T * H * D, 0
     tree_bytes = 2 * T * D * (2 * H + 2 * Hkv)          # Q + O at H, tree K + V at Hkv
     prefix_bytes = 2 * 2 * B * L * Hkv * D                 # prefix K + V at Hkv
     # attended (query, key) pairs per sequence: min(depth, d) + 1 per node
@@ -266,6 +272,7 @@ def main():
     seed = B * 10000 + b * 100 + d
     bhnd = c.get("layout") == "bhnd"
     paged = c.get("layout") == "paged"
+    merge = c.get("layout") == "merge"
     sets = []
     for i in range(nsets):
         Q, K, V, Kp, Vp = make_set(c, seed + i, torch.float16)
@@ -281,6 +288,13 @@ def main():
             K, V = torch.empty_like(Kc), torch.empty_like(Vc)
             K[perm], V[perm] = Kc, Vc
             Kp = perm.to(torch.int32)[pt.long()]  # the page table rides in the prefix slot
+        if merge:
+            # out_pre, out_tree [B, H, Nq, D]; the LSEs ride in the prefix slots
+            g = torch.Generator().manual_seed(seed + i)
+            Q = Q.view(B, N, H, D).permute(0, 2, 1, 3).contiguous()
+            K = K.view(B, N, H, D).permute(0, 2, 1, 3).contiguous()
+            Kp = torch.randn(B, H, N, generator=g) * 3
+            Vp = torch.randn(B, H, N, generator=g) * 3
         sets.append([t.to(dev) if t is not None else None for t in (Q, K, V, Kp, Vp)])
     cu = torch.arange(0, (B + 1) * N, N, dtype=torch.int32, device=dev)
     parents = torch.tensor(tree_parents(c) * B, dtype=torch.int32, device=dev) if parents_walk else None
@@ -292,6 +306,8 @@ def main():
             return ra.ragged_tree_attn(Q, K, V, b, d, parents[:N] if parents_walk else None)
         if paged:
             return ra.ragged_attention_paged(Q, K, V, Kp, cu, b, d, max_seqlen=N)
+        if merge:
+            return ra.fused_lse_merge(Kp, Vp, Q, K)
         if L:
             return ra.ragged_attention_prefix(Q, K, V, cu, Kp, Vp, b, d, max_seqlen=N)
         if parents_walk:
@@ -362,7 +378,7 @@ def main():
     roofline.update({"traffic": traffic, "algorithmic_bytes": alg_bytes, "flops": flops})
 
     cpu = None
-    if not args.no_cpu_baseline:
+    if not args.no_cpu_baseline and not merge:  # (the merge has no padded-SDPA counterpart)
         cpu = cpu_baseline(c)
 
     out = {
@@ -382,7 +398,8 @@ def main():
         "config": {"workload": f"{args.config}: verify attention B={B} b={b} d={d} N={N} H={H} Hkv={Hkv} "
                                f"D={D} L={L} fp16" + (", explicit parents" if parents_walk else "")
                                + (", [B, H, N, D] views" if bhnd else "")
-                               + (", paged K/V (16-token pages, shuffled)" if paged else ""), "B": B, "b": b, "d": d, "N": N, "H": H, "Hkv": Hkv,
+                               + (", paged K/V (16-token pages, shuffled)" if paged else "")
+                               + (", fused_lse_merge of two [B, H, Nq, D] blocks" if merge else ""), "B": B, "b": b, "d": d, "N": N, "H": H, "Hkv": Hkv,
                    "D": D, "L": L, "tokens": T, "algo": args.algo},
         "achieved_GBps": round(achieved_bw / 1e9, 1),
         "wall_us_per_call": round(wall_us, 2),

@@ -67,6 +67,9 @@ def test_prefix_configs():
     assert alg_bytes == 2 * 60 * 128 * (2 * 32 + 2 * 8) + 2 * 2 * 2048 * 8 * 128 == 9_617_408
     assert prefix_flops == 4 * 60 * 32 * 2048 * 128
     assert flops - prefix_flops == 4 * 128 * 32 * sum(x + 1 for x in depth)
+    # merge4: two O blocks + two fp32 LSEs read, one O written
+    T = 4 * 85
+    assert bench.model_costs(bench.CONFIGS["merge4"])[0] == 3 * 2 * T * 32 * 128 + 2 * 4 * T * 32
     # the same workload in other layouts costs the same
     assert bench.model_costs(bench.CONFIGS["cfg4_bhnd"]) == bench.model_costs(bench.CONFIGS["cfg4"])
     assert bench.model_costs(bench.CONFIGS["cfg2_paged"]) == bench.model_costs(bench.CONFIGS["cfg2"])
