@@ -1,26 +1,36 @@
 """Benchmark of the tree-verify attention hot path on one MI355X.
 
-    python bench.py [--steps K] [--warmup W] [--config cfg2|cfg3|cfg4|cfg5|gen1024|cfg4_bhnd|cfg2_paged|eagle3|merge4] [--algo auto|gather|subtree]
+    python bench.py [--steps K] [--warmup W] [--config cfg2|cfg3|cfg4|cfg4_prefix|cfg5|gen1024|cfg4_bhnd|cfg2_paged|eagle3|merge4]
+                    [--algo auto|gather|subtree] [--no-extra] [--no-cpu-baseline]
 
 A step is one full verify-attention call (all sequences, all heads, and the
 prefix KV cache when the config has one) over one batch of synthetic input,
 what the reference times per call (scripts/benchmark_micro.py:585-609).
 Inputs are drawn on the CPU with the reference seed convention
-(B*10000 + b*100 + d), copied to HBM before timing, and rotated over several
-independent sets whose total exceeds 512 MB, so MI355X's 256 MB Infinity
-Cache cannot serve a call from the previous call's data.  The calls are
-captured in HIP graphs (the reference times CUDA-graph replays,
-scripts/benchmark_micro.py:169-187), 8 calls per graph so graph-launch gaps do
-not pad the per-call time.  Before the W warmup steps the graphs are replayed,
-untimed, for SETTLE_S seconds so the GPU's clocks reach their steady state
-(the first ~10 ms of back-to-back calls run up to 5% slower); the timed
-region replays graphs for exactly K calls, bracketed by
-torch.cuda.synchronize().
+(B*10000 + b*100 + d, set i adds i), copied to HBM before timing, and every
+call reads a different input set than the call before it: call k of the run
+uses set k mod nsets, with at least 4 sets totalling more than 512 MB (two
+sets when one is larger than 512 MB), so MI355X's 256 MB Infinity Cache holds
+none of a call's inputs when it starts.  The calls are captured in HIP graphs
+(the reference times CUDA-graph replays, scripts/benchmark_micro.py:169-187),
+up to 32 consecutive calls per graph (kernels inside a graph run back to
+back; each graph launch leaves ~8 µs idle, 0.26 µs per call at 32 calls per
+graph); the rotation runs through the graphs.  Before the warmup the
+graphs are replayed, untimed, for SETTLE_S seconds so the GPU's clocks reach
+their steady state; then exactly W warmup calls and exactly K timed calls,
+the timed region bracketed by torch.cuda.synchronize() and HIP events on the
+stream the kernels run on.
 
 Prints ONE JSON line with the driver's fields plus
   roofline      tree-only configs: algorithmic bytes (Q+K+V+O) / kernel time
                 vs 8 TB/s HBM.  Prefix configs: t_min = max(bytes / 8 TB/s,
                 flops / 2.5 PFLOP/s) and frac = t_min / t.
+  hbm_ceiling   (tree-only configs) torch.addcmul over rotating sets with the
+                workload's bytes (3 reads, 1 write): what a plain streaming
+                kernel reaches under the same cache conditions
+  extra         (default cfg2 run) cfg3, the cfg4 verify call, the cfg4
+                prefix-only call (same queries and prefix, no tree keys) and
+                their ratio, each timed the same way
   cpu_baseline  the reference's CPU path (padded SDPA + tree mask, fp32, MATH
                 backend; restated in oracle/sdpa.py) timed on this host's cores
 """
@@ -38,7 +48,7 @@ sys.path.insert(0, ROOT)
 METRIC = "verify-attn µs/call + achieved HBM GB/s, b=4 d=5 N=1365 H=32 D=128 fp16"
 PEAK_HBM = 8.0e12     # B/s, MI355X HBM3E (vendor figure)
 PEAK_MFMA = 2.5e15    # FLOP/s, MI355X dense fp16 MFMA (vendor figure)
-CALLS_PER_GRAPH = 8
+CALLS_PER_GRAPH = 32  # a graph launch leaves ~8 µs between graphs; 32 calls amortise it
 SETTLE_S = 0.1        # untimed replays before the warmup steps (clock settling)
 
 # BASELINE.json configs[1..4], and the explicit-parents workload of the
@@ -67,6 +77,9 @@ CONFIGS = {
     # fused_lse_merge (src/ragged_attn.py:1619-1653) at cfg4's verify shape:
     # two [B, H, Nq, D] blocks and their LSEs merged into one output
     "merge4": dict(B=4, b=4, d=3, H=32, Hkv=32, D=128, L=0, sigma=1.0, layout="merge"),
+    # cfg4's prefix pass alone (prefix_attention: the same queries and prefix,
+    # no tree keys), the denominator of the cfg4 verify/prefix-only ratio
+    "cfg4_prefix": dict(B=4, b=4, d=3, H=32, Hkv=8, D=128, L=10240, sigma=1.0, layout="prefix_only"),
 }
 
 
@@ -130,6 +143,9 @@ def model_costs(c):
         return 3 * 2 * T * H * D + 2 * 4 * T * H, 6 * T * H * D, 0
     tree_bytes = 2 * T * D * (2 * H + 2 * Hkv)          # Q + O at H, tree K + V at Hkv
     prefix_bytes = 2 * 2 * B * L * Hkv * D                 # prefix K + V at Hkv
+    prefix_flops = 4 * B * N * H * L * D
+    if c.get("layout") == "prefix_only":
+        return 2 * T * D * 2 * H + prefix_bytes, prefix_flops, prefix_flops
     # attended (query, key) pairs per sequence: min(depth, d) + 1 per node
     par = tree_parents(c)
     depth = [0] * N
@@ -137,7 +153,6 @@ def model_costs(c):
         depth[i] = depth[par[i]] + 1 if (b > 1 or c.get("walk") == "eagle") else i
     steps = sum(min(x, d) + 1 for x in depth)
     tree_flops = 4 * D * H * B * steps
-    prefix_flops = 4 * B * N * H * L * D
     return tree_bytes + prefix_bytes, tree_flops + prefix_flops, prefix_flops
 
 
@@ -233,6 +248,205 @@ def cpu_baseline(c, budget_s=20.0):
     }
 
 
+def n_sets(alg_bytes, forced=0):
+    """Input sets to rotate: two when one set alone exceeds 512 MB, else at
+    least 4 and enough for 600 MB (at most 64)."""
+    if forced:
+        return forced
+    if alg_bytes > 512_000_000:
+        return 2
+    return min(64, max(4, -(-600_000_000 // alg_bytes)))
+
+
+def rotation_chunks(start, n):
+    """Calls start .. start+n-1 as graphs of up to CALLS_PER_GRAPH consecutive
+    calls: a list of (first call, calls); call k reads set k mod nsets."""
+    out = []
+    while n > 0:
+        m = min(CALLS_PER_GRAPH, n)
+        out.append((start, m))
+        start, n = start + m, n - m
+    return out
+
+
+def time_rotating(call, nsets, steps, warmup):
+    """Time `steps` calls, call k reading input set k mod nsets.
+
+    call(i) launches one call on set i on torch's current stream.  Every set
+    is run eagerly first (on the current stream and on a side stream, as
+    graph capture needs), then the calls are captured in graphs of up to
+    CALLS_PER_GRAPH consecutive calls (one graph per distinct run of sets),
+    replayed untimed for SETTLE_S seconds, then for exactly `warmup` calls and
+    exactly `steps` timed calls that continue the rotation.  Returns
+    (µs per call from HIP events on the stream the graphs replay on,
+     µs per call of host wall time)."""
+    import torch
+    for i in range(nsets):
+        call(i)
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for i in range(nsets):
+            call(i)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graphs = {}
+
+    def graph(start, n):
+        key = (start % nsets, n)
+        if key not in graphs:
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                for k in range(n):
+                    call((start + k) % nsets)
+            graphs[key] = g
+        return graphs[key]
+
+    def plan(start, n):
+        return [graph(s0, m) for s0, m in rotation_chunks(start, n)]
+
+    settle = plan(0, CALLS_PER_GRAPH * nsets)
+    warm = plan(0, warmup)
+    timed = plan(warmup, steps)
+    torch.cuda.synchronize()
+    t_settle = time.perf_counter()
+    k = 0
+    while time.perf_counter() - t_settle < SETTLE_S:
+        settle[k % len(settle)].replay()
+        k += 1
+        if k % 8 == 0:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
+    for g in warm:
+        g.replay()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ev0.record(stream)
+    for g in timed:
+        g.replay()
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    del graphs, settle, warm, timed
+    return ev0.elapsed_time(ev1) * 1e3 / steps, (t1 - t0) / steps * 1e6
+
+
+def build_workload(name, algo, forced_sets=0):
+    """Device input sets of a config and call(i) running one call on set i."""
+    import torch
+    from qattention_amd import ragged_attn as ra
+
+    c = CONFIGS[name]
+    B, b, d, H, Hkv, D, L = (c[k] for k in ("B", "b", "d", "H", "Hkv", "D", "L"))
+    N = tree_size(c)
+    parents_walk = c.get("walk") in ("parents", "eagle")
+    dev = torch.device("cuda:0")
+    alg_bytes, _, _ = model_costs(c)
+    nsets = n_sets(alg_bytes, forced_sets)
+    seed = B * 10000 + b * 100 + d
+    layout = c.get("layout")
+    sets = []
+    for i in range(nsets):
+        Q, K, V, Kp, Vp = make_set(c, seed + i, torch.float16)
+        if layout == "bhnd":
+            # the same values in the E2E layout: prefix rows then tree rows per sequence
+            Q = Q.view(B, N, H, D).permute(0, 2, 1, 3).contiguous()
+            K = torch.cat([Kp, K.view(B, N, Hkv, D)], 1).permute(0, 2, 1, 3).contiguous()
+            V = torch.cat([Vp, V.view(B, N, Hkv, D)], 1).permute(0, 2, 1, 3).contiguous()
+            Kp = Vp = None
+        if layout == "paged":
+            Kc, Vc, pt = ra.build_paged_kv(list(K.view(B, N, Hkv, D)), list(V.view(B, N, Hkv, D)), 16)
+            perm = torch.randperm(Kc.shape[0], generator=torch.Generator().manual_seed(seed + i))
+            K, V = torch.empty_like(Kc), torch.empty_like(Vc)
+            K[perm], V[perm] = Kc, Vc
+            Kp = perm.to(torch.int32)[pt.long()]  # the page table rides in the prefix slot
+        if layout == "merge":
+            # out_pre, out_tree [B, H, Nq, D]; the LSEs ride in the prefix slots
+            g = torch.Generator().manual_seed(seed + i)
+            Q = Q.view(B, N, H, D).permute(0, 2, 1, 3).contiguous()
+            K = K.view(B, N, H, D).permute(0, 2, 1, 3).contiguous()
+            Kp = torch.randn(B, H, N, generator=g) * 3
+            Vp = torch.randn(B, H, N, generator=g) * 3
+        if layout == "prefix_only":
+            K = V = None  # no tree keys
+        sets.append([t.to(dev) if t is not None else None for t in (Q, K, V, Kp, Vp)])
+    cu = torch.arange(0, (B + 1) * N, N, dtype=torch.int32, device=dev)
+    parents = torch.tensor(tree_parents(c) * B, dtype=torch.int32, device=dev) if parents_walk else None
+    torch.cuda.synchronize()
+
+    def call(i):
+        Q, K, V, Kp, Vp = sets[i]
+        if layout == "bhnd":
+            return ra.ragged_tree_attn(Q, K, V, b, d, parents[:N] if parents_walk else None)
+        if layout == "paged":
+            return ra.ragged_attention_paged(Q, K, V, Kp, cu, b, d, max_seqlen=N)
+        if layout == "merge":
+            return ra.fused_lse_merge(Kp, Vp, Q, K)
+        if layout == "prefix_only":
+            return ra.prefix_attention(Q, Kp, Vp, cu, max_seqlen=N)
+        if L:
+            return ra.ragged_attention_prefix(Q, K, V, cu, Kp, Vp, b, d, max_seqlen=N)
+        if parents_walk:
+            return ra.ragged_attention_with_parents(Q, K, V, cu, parents, d, max_seqlen=N)[0]
+        return ra._tree_forward(Q, K, V, cu, b, d, N, False, algo)[0]
+
+    return call, nsets
+
+
+def roofline_of(c, t_us):
+    alg_bytes, flops, prefix_flops = model_costs(c)
+    t_s = t_us * 1e-6
+    achieved_bw = alg_bytes / t_s
+    if c["L"]:
+        t_min = max(alg_bytes / PEAK_HBM, flops / PEAK_MFMA)
+        bound = "mfma" if flops / PEAK_MFMA >= alg_bytes / PEAK_HBM else "hbm"
+        return {"bound": bound, "achieved": round(flops / t_s / 1e12, 1) if bound == "mfma"
+                else round(achieved_bw / 1e9, 1),
+                "peak": PEAK_MFMA / 1e12 if bound == "mfma" else PEAK_HBM / 1e9,
+                "unit": "TFLOP/s" if bound == "mfma" else "GB/s",
+                "frac": round(t_min / t_s, 4), "t_min_us": round(t_min * 1e6, 2),
+                "hbm_frac": round(achieved_bw / PEAK_HBM, 4),
+                "mfma_frac": round(flops / t_s / PEAK_MFMA, 4)}
+    return {"bound": "hbm", "achieved": round(achieved_bw / 1e9, 1), "peak": PEAK_HBM / 1e9,
+            "unit": "GB/s", "frac": round(achieved_bw / PEAK_HBM, 4)}
+
+
+def hbm_ceiling(alg_bytes, steps, warmup):
+    """torch.addcmul(a, b, c) -> o over rotating sets, 4 tensors of alg_bytes/4
+    each (3 reads, 1 write, the tree workloads' Q+K+V read and O write):
+    a plain streaming kernel's rate under the same cache conditions."""
+    import torch
+    n = alg_bytes // 4 // 2
+    nsets = n_sets(alg_bytes)
+    dev = torch.device("cuda:0")
+    sets = [[torch.empty(n, dtype=torch.float16, device=dev).normal_() for _ in range(4)] for _ in range(nsets)]
+
+    def call(i):
+        a, b, c, o = sets[i]
+        torch.addcmul(a, b, c, out=o)
+
+    us, _ = time_rotating(call, nsets, steps, warmup)
+    del sets
+    torch.cuda.empty_cache()
+    return {"kernel": "torch.addcmul fp16, 3 reads + 1 write of the workload's bytes, rotating sets",
+            "us": round(us, 2), "GBps": round(alg_bytes / us / 1e3, 1),
+            "frac": round(alg_bytes / (us * 1e-6) / PEAK_HBM, 4)}
+
+
+def measure(name, algo, steps, warmup, forced_sets=0):
+    """(µs per call from events, µs per call of wall time, input sets)."""
+    import torch
+    call, nsets = build_workload(name, algo, forced_sets)
+    us, wall = time_rotating(call, nsets, steps, warmup)
+    del call
+    torch.cuda.empty_cache()
+    return us, wall, nsets
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -241,7 +455,9 @@ def main():
     ap.add_argument("--config", default="cfg2", choices=sorted(CONFIGS))
     ap.add_argument("--algo", default="auto", choices=["auto", "gather", "subtree"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--sets", type=int, default=0, help="rotating input sets (0: enough for > 512 MB)")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="cfg2 only: skip the extra timings (cfg3, cfg4 verify / prefix-only, HBM ceiling)")
+    ap.add_argument("--sets", type=int, default=0, help="rotating input sets (0: see n_sets)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain MIB-MiB device copy (counter calibration) and exit")
     args = ap.parse_args()
@@ -253,140 +469,54 @@ def main():
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
               "the tree path shards over sequences/heads with no exchange between GPUs", file=sys.stderr)
         sys.exit(2)
+    if args.steps < 1 or args.warmup < 0:
+        print("bench.py: --steps must be >= 1 and --warmup >= 0", file=sys.stderr)
+        sys.exit(2)
 
     import torch
     from qattention_amd import _lib
-    from qattention_amd import ragged_attn as ra
 
+    torch.cuda.set_device(torch.device("cuda:0"))
+    algo = {"auto": _lib.ALGO_AUTO, "gather": _lib.ALGO_GATHER, "subtree": _lib.ALGO_SUBTREE}[args.algo]
     c = CONFIGS[args.config]
     B, b, d, H, Hkv, D, L = (c[k] for k in ("B", "b", "d", "H", "Hkv", "D", "L"))
     N = tree_size(c)
     T = B * N
+    layout = c.get("layout")
     parents_walk = c.get("walk") in ("parents", "eagle")
-    dev = torch.device("cuda:0")
-    torch.cuda.set_device(dev)
-    algo = {"auto": _lib.ALGO_AUTO, "gather": _lib.ALGO_GATHER, "subtree": _lib.ALGO_SUBTREE}[args.algo]
-    alg_bytes, flops, prefix_flops = model_costs(c)
-    nsets = args.sets or max(2, min(8, -(-600_000_000 // alg_bytes)))
+    alg_bytes, flops, _ = model_costs(c)
 
-    seed = B * 10000 + b * 100 + d
-    bhnd = c.get("layout") == "bhnd"
-    paged = c.get("layout") == "paged"
-    merge = c.get("layout") == "merge"
-    sets = []
-    for i in range(nsets):
-        Q, K, V, Kp, Vp = make_set(c, seed + i, torch.float16)
-        if bhnd:
-            # the same values in the E2E layout: prefix rows then tree rows per sequence
-            Q = Q.view(B, N, H, D).permute(0, 2, 1, 3).contiguous()
-            K = torch.cat([Kp, K.view(B, N, Hkv, D)], 1).permute(0, 2, 1, 3).contiguous()
-            V = torch.cat([Vp, V.view(B, N, Hkv, D)], 1).permute(0, 2, 1, 3).contiguous()
-            Kp = Vp = None
-        if paged:
-            Kc, Vc, pt = ra.build_paged_kv(list(K.view(B, N, Hkv, D)), list(V.view(B, N, Hkv, D)), 16)
-            perm = torch.randperm(Kc.shape[0], generator=torch.Generator().manual_seed(seed + i))
-            K, V = torch.empty_like(Kc), torch.empty_like(Vc)
-            K[perm], V[perm] = Kc, Vc
-            Kp = perm.to(torch.int32)[pt.long()]  # the page table rides in the prefix slot
-        if merge:
-            # out_pre, out_tree [B, H, Nq, D]; the LSEs ride in the prefix slots
-            g = torch.Generator().manual_seed(seed + i)
-            Q = Q.view(B, N, H, D).permute(0, 2, 1, 3).contiguous()
-            K = K.view(B, N, H, D).permute(0, 2, 1, 3).contiguous()
-            Kp = torch.randn(B, H, N, generator=g) * 3
-            Vp = torch.randn(B, H, N, generator=g) * 3
-        sets.append([t.to(dev) if t is not None else None for t in (Q, K, V, Kp, Vp)])
-    cu = torch.arange(0, (B + 1) * N, N, dtype=torch.int32, device=dev)
-    parents = torch.tensor(tree_parents(c) * B, dtype=torch.int32, device=dev) if parents_walk else None
-    torch.cuda.synchronize()
+    event_us, wall_us, nsets = measure(args.config, algo, args.steps, args.warmup, args.sets)
+    roofline = roofline_of(c, event_us)
+    roofline.update({"traffic": measured_traffic(args.config), "algorithmic_bytes": alg_bytes, "flops": flops})
 
-    def call(i):
-        Q, K, V, Kp, Vp = sets[i]
-        if bhnd:
-            return ra.ragged_tree_attn(Q, K, V, b, d, parents[:N] if parents_walk else None)
-        if paged:
-            return ra.ragged_attention_paged(Q, K, V, Kp, cu, b, d, max_seqlen=N)
-        if merge:
-            return ra.fused_lse_merge(Kp, Vp, Q, K)
-        if L:
-            return ra.ragged_attention_prefix(Q, K, V, cu, Kp, Vp, b, d, max_seqlen=N)
-        if parents_walk:
-            return ra.ragged_attention_with_parents(Q, K, V, cu, parents, d, max_seqlen=N)[0]
-        return ra._tree_forward(Q, K, V, cu, b, d, N, False, algo)[0]
-
-    for i in range(nsets):
-        call(i)
-    torch.cuda.synchronize()
-    side = torch.cuda.Stream()
-    side.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(side):
-        for i in range(nsets):
-            call(i)
-    torch.cuda.current_stream().wait_stream(side)
-    torch.cuda.synchronize()
-    # one graph per input set, CALLS_PER_GRAPH calls each
-    graphs = []
-    for i in range(nsets):
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
-            for _ in range(CALLS_PER_GRAPH):
-                call(i)
-        graphs.append(g)
-    replays = max(1, -(-args.steps // CALLS_PER_GRAPH))
-    steps = replays * CALLS_PER_GRAPH
-    t_settle = time.perf_counter()
-    k = 0
-    while time.perf_counter() - t_settle < SETTLE_S:
-        graphs[k % nsets].replay()
-        k += 1
-        if k % 8 == 0:
-            torch.cuda.synchronize()
-    torch.cuda.synchronize()
-    for k in range(max(1, args.warmup // CALLS_PER_GRAPH)):
-        graphs[k % nsets].replay()
-    torch.cuda.synchronize()
-
-    stream = torch.cuda.current_stream()
-    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    ev0.record(stream)
-    for k in range(replays):
-        graphs[k % nsets].replay()
-    ev1.record(stream)
-    torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    wall_us = (t1 - t0) / steps * 1e6
-    event_us = ev0.elapsed_time(ev1) * 1e3 / steps
-
-    t_s = event_us * 1e-6
-    achieved_bw = alg_bytes / t_s
-    if L:
-        t_min = max(alg_bytes / PEAK_HBM, flops / PEAK_MFMA)
-        bound = "mfma" if flops / PEAK_MFMA >= alg_bytes / PEAK_HBM else "hbm"
-        roofline = {"bound": bound, "achieved": round(flops / t_s / 1e12, 1) if bound == "mfma"
-                    else round(achieved_bw / 1e9, 1),
-                    "peak": PEAK_MFMA / 1e12 if bound == "mfma" else PEAK_HBM / 1e9,
-                    "unit": "TFLOP/s" if bound == "mfma" else "GB/s",
-                    "frac": round(t_min / t_s, 4), "t_min_us": round(t_min * 1e6, 2),
-                    "hbm_frac": round(achieved_bw / PEAK_HBM, 4),
-                    "mfma_frac": round(flops / t_s / PEAK_MFMA, 4)}
-    else:
-        roofline = {"bound": "hbm", "achieved": round(achieved_bw / 1e9, 1), "peak": PEAK_HBM / 1e9,
-                    "unit": "GB/s", "frac": round(achieved_bw / PEAK_HBM, 4)}
-    traffic = measured_traffic(args.config)
-    roofline.update({"traffic": traffic, "algorithmic_bytes": alg_bytes, "flops": flops})
+    extra = None
+    ceiling = None
+    if not L and layout != "merge":
+        ceiling = hbm_ceiling(alg_bytes, args.steps, args.warmup)
+    if args.config == "cfg2" and not args.no_extra:
+        extra = {}
+        us3, _, _ = measure("cfg3", algo, args.steps, args.warmup)
+        extra.update({"cfg3_us": round(us3, 2), "cfg3_hbm_frac": roofline_of(CONFIGS["cfg3"], us3)["frac"]})
+        us4, _, _ = measure("cfg4", _lib.ALGO_AUTO, args.steps, args.warmup)
+        us4p, _, _ = measure("cfg4_prefix", _lib.ALGO_AUTO, args.steps, args.warmup)
+        extra.update({"cfg4_verify_us": round(us4, 2), "cfg4_prefix_only_us": round(us4p, 2),
+                      "cfg4_ratio": round(us4 / us4p, 3),
+                      "cfg4_frac": roofline_of(CONFIGS["cfg4"], us4)["frac"],
+                      "cfg4_prefix_only_frac": roofline_of(CONFIGS["cfg4_prefix"], us4p)["frac"]})
 
     cpu = None
-    if not args.no_cpu_baseline and not merge:  # (the merge has no padded-SDPA counterpart)
+    if not args.no_cpu_baseline and layout not in ("merge", "prefix_only"):
+        # (the merge and the prefix pass alone have no padded-SDPA tree counterpart)
         cpu = cpu_baseline(c)
 
+    achieved_bw = alg_bytes / (event_us * 1e-6)
     out = {
         "metric": METRIC,
         "value": round(event_us, 2),
         "unit": "us/call",
         "n_gpus": 1,
-        "steps": steps,
+        "steps": args.steps,
         "warmup": args.warmup,
         "settle_s": SETTLE_S,
         "ms_per_step": round(wall_us / 1e3, 5),
@@ -394,16 +524,21 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f16",
-        "data": f"synthetic N(0,{c['sigma']}^2), CPU-seeded (seed B*10000+b*100+d), {nsets} rotating sets",
+        "data": (f"synthetic N(0,{c['sigma']}^2), CPU-seeded (seed B*10000+b*100+d + set), {nsets} input sets "
+                 "rotated call by call"),
         "config": {"workload": f"{args.config}: verify attention B={B} b={b} d={d} N={N} H={H} Hkv={Hkv} "
                                f"D={D} L={L} fp16" + (", explicit parents" if parents_walk else "")
-                               + (", [B, H, N, D] views" if bhnd else "")
-                               + (", paged K/V (16-token pages, shuffled)" if paged else "")
-                               + (", fused_lse_merge of two [B, H, Nq, D] blocks" if merge else ""), "B": B, "b": b, "d": d, "N": N, "H": H, "Hkv": Hkv,
+                               + (", [B, H, N, D] views" if layout == "bhnd" else "")
+                               + (", paged K/V (16-token pages, shuffled)" if layout == "paged" else "")
+                               + (", fused_lse_merge of two [B, H, Nq, D] blocks" if layout == "merge" else "")
+                               + (", prefix pass only (no tree keys)" if layout == "prefix_only" else ""),
+                   "B": B, "b": b, "d": d, "N": N, "H": H, "Hkv": Hkv,
                    "D": D, "L": L, "tokens": T, "algo": args.algo},
         "achieved_GBps": round(achieved_bw / 1e9, 1),
         "wall_us_per_call": round(wall_us, 2),
         "roofline": roofline,
+        "hbm_ceiling": ceiling,
+        "extra": extra,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

@@ -5,18 +5,23 @@
  * Every entry point takes plain device pointers, element strides and sizes,
  * launches asynchronously on the given HIP stream (hipStream_t passed as
  * void*, NULL = the legacy default stream) and is HIP-graph capturable.
- * Outputs and workspaces belong to the caller.  The library's one allocation
- * is a 2 MiB pool of work-schedule counters per device, allocated and zeroed
- * (synchronously) by the first uncaptured call that launches the subtree
- * kernel on that device, and kept until the process ends; every launch
- * leaves its counters at zero.  Uncaptured launches take the pool's 32 eager
- * slots in turn, so up to 32 of them may be in flight at once per device
- * (on different streams).  A launch recorded into a graph keeps a slot of
- * its own, 96 per device per process; past that, or while the first call on
- * a device is being recorded, recorded launches use a static schedule (same
- * results, slower).  Two graph executables instantiated from one capture
- * share its slots and must not run at the same time.  Calls are
- * thread-safe (the pool is guarded by a mutex).
+ * Outputs and workspaces belong to the caller.  No entry point allocates
+ * memory, synchronises or zeroes anything behind the caller's back.
+ *
+ * The subtree kernel's work-schedule counters live in a static device array
+ * (2 MiB per device, part of the library's code object).  qattn_init() sets
+ * it up on the current device; until then every launch on that device runs
+ * the static schedule (same results, slower).  Each launch leaves its
+ * counters at zero.  A counter slot only serves launches that cannot overlap:
+ *   - an uncaptured launch uses the slot of its stream (launches on one
+ *     stream run in order); 64 streams per device get a slot, launches on
+ *     further streams run the static schedule;
+ *   - a launch recorded into a graph keeps a slot of its own for every
+ *     replay (replays of one graph executable run in order); after 192 such
+ *     launches per device, further recorded launches use the static schedule.
+ *     As with any memory a capture records, two graph executables
+ *     instantiated from one capture must not run at the same time.
+ * Calls are thread-safe (the slot table is guarded by a mutex).
  * Return value: QATTN_OK (0) or a negative QATTN_ERR_* code; the message of
  * the last failure on the calling thread is qattn_last_error().
  *
@@ -35,8 +40,9 @@
  *     max_seqlen bounds every sequence length (tokens at or beyond it are not
  *     computed).  A sequence whose offsets are decreasing, negative or beyond
  *     total_tokens is skipped (its output rows are left untouched).
- *   - scale multiplies q.k (the reference fixes it to 1/sqrt(head_dim));
- *     the prefix entry points require scale > 0.
+ *   - scale multiplies q.k (the reference fixes it to 1/sqrt(head_dim)); the
+ *     tree-only entry points take any finite scale, the prefix entry points
+ *     require scale > 0.
  *   - lse (optional, may be NULL) is fp32 [tokens, num_q_heads] with strides
  *     {stride_token, stride_head}: lse = m + ln(sum exp(s - m)).
  */
@@ -67,6 +73,16 @@ extern "C" {
 
 /* Library version string. */
 const char *qattn_version(void);
+
+/*
+ * Set up the library on the CURRENT device (no reference counterpart: the
+ * Triton module has no device state).  Looks up the device address of the
+ * schedule-counter array and zeroes it, synchronously, on a private stream.
+ * Call it once per device before the first attention call there, outside
+ * graph capture; later calls return at once.  Without it every call still
+ * works, with the subtree kernel on its static schedule.
+ */
+int qattn_init(void);
 
 /* Message of the last failed call on this thread ("" if none). */
 const char *qattn_last_error(void);
@@ -150,6 +166,25 @@ int qattn_ancestors(const int32_t *cu_seqlens, const int32_t *parents, int32_t b
                     int32_t max_depth, int32_t *out, void *stream);
 
 /*
+ * Walk export, a test hook (no reference counterpart; it exposes the walk of
+ * src/ragged_attn.py:323-377 / :650-698 as each kernel executes it).  While
+ * out is non-null, the attention calls made on the calling thread run their
+ * kernels' walk-export instantiations: the same outputs, plus, for every
+ * query (packed token t, q head h) they compute, the ancestor set the
+ * kernel used, out[(t * num_q_heads + h) * (max_depth + 1) + i] = the node
+ * attended at walk step i, or -1.  Subtree kernel: the query's row mask
+ * decoded through the row map its K/V loads were issued with; gather walk:
+ * the node each step loads; fused prefix epilogue: the node of the staged
+ * LDS row each step reads.  -2 at step 0 marks an inconsistency (a mask bit
+ * on a row without a node, two rows at one step, a Q row staged from another
+ * query).  Entries of queries no kernel computes are left as they were.
+ * Only fp16 calls over packed cu_seqlens without LSE (else QATTN_ERR_ARG);
+ * out is a DEVICE int32 array of total_tokens * num_q_heads * (max_depth+1)
+ * entries.  NULL turns it off.
+ */
+int qattn_debug_walk(int32_t *out);
+
+/*
  * Tree-verify attention with a prefix KV cache that every tree query attends
  * in full, plus its own ancestors among the tree tokens.
  *
@@ -192,6 +227,31 @@ int qattn_prefix_tree_fwd(const void *q, const int64_t q_stride[3],
                           int32_t branching_factor, int32_t max_depth, float scale,
                           int32_t dtype, void *workspace, int64_t workspace_size,
                           int32_t num_splits, void *stream);
+
+/*
+ * Attention of query tokens over a prefix KV cache only (no tree keys), with
+ * LSE: the prefix pass of the reference's verify pipelines, in the layout of
+ * qattn_prefix_tree_fwd, GQA-native.
+ *
+ * Replaces flashinfer.single_prefill_with_kv_cache_return_lse as the
+ * reference benchmark calls it (scripts/benchmark_micro.py:574-580, a prefix
+ * [L, H, D] shared by every query: kp_stride[0] == 0) and the aten flash
+ * prefix pass with LSE of the E2E verify step (scripts/e2e_benchmark.py:
+ * 1438-1448, one prefix per sequence).  Query token t of sequence s (rows
+ * cu_seqlens[s] .. cu_seqlens[s+1]-1) attends all prefix_len >= 1 rows of
+ * sequence s's prefix.  Workspace sized by qattn_prefix_workspace_bytes()
+ * with the same arguments; the split count and prefix kernel are those of
+ * qattn_prefix_tree_fwd, so the two calls time the prefix alone and the
+ * prefix plus tree.
+ */
+int qattn_prefix_fwd(const void *q, const int64_t q_stride[3],
+                     const void *k_prefix, const int64_t kp_stride[3],
+                     const void *v_prefix, const int64_t vp_stride[3], int32_t prefix_len,
+                     void *o, const int64_t o_stride[3], float *lse, const int64_t lse_stride[2],
+                     const int32_t *cu_seqlens, int32_t batch, int32_t max_seqlen,
+                     int64_t total_tokens, int32_t num_q_heads, int32_t num_kv_heads,
+                     int32_t head_dim, float scale, int32_t dtype, void *workspace,
+                     int64_t workspace_size, int32_t num_splits, void *stream);
 
 /*
  * The same over an explicit parent array (EAGLE-3 dynamic trees) instead of a

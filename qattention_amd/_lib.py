@@ -5,10 +5,11 @@ no fallback: if it is missing, every call raises.
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes as C
 import os
 
-import torch  # noqa: F401  -- must be loaded first so libqattn.so binds torch's HIP runtime
+import torch  # must be loaded first so libqattn.so binds torch's HIP runtime
 
 from .build import LIB_PATH
 
@@ -37,6 +38,8 @@ _i64p = C.POINTER(C.c_int64)
 SIGNATURES = {
     "qattn_version": (C.c_char_p, []),
     "qattn_last_error": (C.c_char_p, []),
+    "qattn_init": (C.c_int, []),
+    "qattn_debug_walk": (C.c_int, [_p]),
     "qattn_tree_fwd": (C.c_int, [
         _p, _i64p, _p, _i64p, _p, _i64p, _p, _i64p, _p, _i64p,
         _p, _i32, _i32, _i64, _i32, _i32, _i32, _i32, _i32, _f32, _i32, _i32, _p]),
@@ -52,6 +55,9 @@ SIGNATURES = {
         _p, _i64p, _p, _i64p, _p, _i64p, _p, _i64p, _p, _i64p, _i32,
         _p, _i64p, _p, _i64p, _p, _i32, _i32, _i64, _i64, _i64,
         _i32, _i32, _i32, _i32, _i32, _f32, _i32, _p, _i64, _i32, _p]),
+    "qattn_prefix_fwd": (C.c_int, [
+        _p, _i64p, _p, _i64p, _p, _i64p, _i32, _p, _i64p, _p, _i64p,
+        _p, _i32, _i32, _i64, _i32, _i32, _i32, _f32, _i32, _p, _i64, _i32, _p]),
     "qattn_prefix_tree_parents_fwd": (C.c_int, [
         _p, _i64p, _p, _i64p, _p, _i64p, _p, _i64p, _p, _i64p, _i32,
         _p, _i64p, _p, _i64p, _p, _p, _i32, _i32, _i64, _i64, _i64,
@@ -86,6 +92,35 @@ def lib():
             fn.argtypes = args
         _lib = L
     return _lib
+
+
+_initialised = set()
+
+
+def ensure_init(device) -> None:
+    """qattn_init() once per device, outside graph capture (the library then
+    gives the subtree kernel its schedule counters on that device; a call
+    made before it, e.g. the first one inside a capture, runs the static
+    schedule)."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    if idx in _initialised or torch.cuda.is_current_stream_capturing():
+        return
+    with torch.cuda.device(idx):
+        check(lib().qattn_init(), "qattn_init")
+    _initialised.add(idx)
+
+
+@contextlib.contextmanager
+def debug_walk(table):
+    """While active, attention calls on this thread also write the ancestor
+    set each query attended, as the kernels used it, into `table` (a device
+    int32 tensor [total_tokens, num_q_heads, max_depth + 1]; see
+    qattn_debug_walk in include/qattn.h)."""
+    check(lib().qattn_debug_walk(table.data_ptr()), "qattn_debug_walk")
+    try:
+        yield table
+    finally:
+        lib().qattn_debug_walk(None)
 
 
 def last_error() -> str:

@@ -17,6 +17,7 @@ import sys
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(PKG_DIR, "csrc")
 LIB_PATH = os.path.join(PKG_DIR, "libqattn.so")
+OBJ_DIR = os.path.join(PKG_DIR, "_build")
 SOURCES = ["tree_attn.hip", "subtree_stream.hip", "prefix_attn.hip"]
 HEADERS = ["qattn_common.h", "qattn_device.h", "tree_walk.h"]
 ARCH = os.environ.get("QATTN_ARCH", "gfx950")
@@ -42,20 +43,37 @@ def compile_flags() -> list:
     ]
 
 
-def build(verbose: bool = True) -> str:
-    """Compile every HIP source into qattention_amd/libqattn.so (always rebuilds)."""
-    srcs = [os.path.join(CSRC, s) for s in SOURCES]
-    tmp = LIB_PATH + ".tmp"
-    cmd = [_hipcc(), *compile_flags(), "-shared", "-o", tmp, *srcs]
+def _run(cmd, verbose):
     if verbose:
         print("[qattention_amd.build]", " ".join(cmd), flush=True)
-    proc = subprocess.run(cmd, capture_output=True, text=True)
+    return subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True)
+
+
+def _finish(proc, verbose):
+    _, stderr = proc.communicate()
     noise = "is not a recognized feature for this target"
-    err = "\n".join(l for l in proc.stderr.splitlines() if noise not in l)
+    err = "\n".join(l for l in stderr.splitlines() if noise not in l)
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{err}")
     if verbose and err.strip():
         print(err, file=sys.stderr)
+
+
+def build(verbose: bool = True) -> str:
+    """Compile every HIP source into qattention_amd/libqattn.so (always rebuilds).
+
+    Each source is compiled to an object in its own hipcc process (they run
+    in parallel), then the objects are linked into the shared library."""
+    os.makedirs(OBJ_DIR, exist_ok=True)
+    objs, procs = [], []
+    for s in SOURCES:
+        obj = os.path.join(OBJ_DIR, os.path.splitext(s)[0] + ".o")
+        objs.append(obj)
+        procs.append(_run([_hipcc(), *compile_flags(), "-c", "-o", obj, os.path.join(CSRC, s)], verbose))
+    for proc in procs:
+        _finish(proc, verbose)
+    tmp = LIB_PATH + ".tmp"
+    _finish(_run([_hipcc(), f"--offload-arch={ARCH}", "-shared", "-o", tmp, *objs], verbose), verbose)
     os.replace(tmp, LIB_PATH)
     return LIB_PATH
 

@@ -67,9 +67,11 @@ __device__ __forceinline__ int kv_swz(int r, int dv) {
 // s_waitcnt immediate (gfx9 encoding): vmcnt N, expcnt and lgkmcnt unconstrained
 constexpr int kWaitVm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 
-// WALK: the tree walk of the fused epilogue (heap or explicit parents); the
-// split kernels leave the walk to the tree kernels.
-template <typename T, int D, bool FUSED, bool LSE, int WALK, bool BATCH>
+// WALK: the tree walk of the fused epilogue (heap or explicit parents, or
+// none for the prefix-only pass); the split kernels leave the walk to the tree
+// kernels.  DBG: the walk-export instantiation (qattn_debug_walk), which also
+// writes each query's attended ancestors to tp.dbg_walk.
+template <typename T, int D, bool FUSED, bool LSE, int WALK, bool BATCH, bool DBG = false>
 __global__ __launch_bounds__(kPrefixThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefix_attn_kernel(
     PrefixParams p, TreeParams tp) {
     constexpr int NC = D / 32;      // MFMA k-chunks over the head dim
@@ -83,6 +85,8 @@ __global__ __launch_bounds__(kPrefixThreads) __attribute__((amdgpu_waves_per_eu(
     // compiler tells them apart: a read of one buffer does not wait for the
     // LDS-DMA loads in flight into another.
     __shared__ __attribute__((aligned(1024))) uint16_t Kb0[BLK], Kb1[BLK], Vb0[BLK], Vb1[BLK];
+    // DBG only: the node of each row the epilogue stages in LDS
+    __shared__ int32_t dbg_slot[DBG ? 2 * (BLK / D) : 1];
     auto kbuf = [&](auto i) -> uint16_t* {
         if constexpr (decltype(i)::value == 0) return Kb0; else return Kb1;
     };
@@ -479,8 +483,9 @@ __global__ __launch_bounds__(kPrefixThreads) __attribute__((amdgpu_waves_per_eu(
             // query grp's state is held by lane grp of the MFMA layout (l16 = grp, lq = 0)
             mw[b] = __shfl(m_run[b], grp);
             lw[b] = __shfl(l_tot[b], grp);
-            load_q4<D, BATCH>(tp, seq, qrb[b], hb[b], j, qf4[b]);
+            if constexpr (WALK != WALK_NONE) load_q4<D, BATCH>(tp, seq, qrb[b], hb[b], j, qf4[b]);
         }
+        if constexpr (WALK != WALK_NONE) {  // (prefix only: nothing to walk)
         // Heap parents are monotonic, so walk step t of every token in the
         // tile's range [tl, th] lies in [par^t(tl), par^t(th)].  When those
         // ranges (steps 1 ..) total at most 128 rows they are staged once in
@@ -502,6 +507,17 @@ __global__ __launch_bounds__(kPrefixThreads) __attribute__((amdgpu_waves_per_eu(
                 hi = heap_parent(hi, tp.bdiv);
                 total += hi - lo + 1;
                 nlev = t;
+            }
+        }
+        // (DBG: lane 0 of each query's group owns the query's export row)
+        int32_t* dbg[kQB] = {};
+        if constexpr (DBG) {
+#pragma unroll
+            for (int b = 0; b < kQB; ++b) {
+                if (vb[b] && j == 0) {
+                    dbg[b] = tp.dbg_walk + (qrb[b] * tp.Hq + hb[b]) * (tp.max_depth + 1);
+                    for (int i = 0; i <= tp.max_depth; ++i) dbg[b][i] = -1;
+                }
             }
         }
         if (WALK == WALK_HEAP && total <= kLdsRows) {
@@ -531,6 +547,9 @@ __global__ __launch_bounds__(kPrefixThreads) __attribute__((amdgpu_waves_per_eu(
                         const int64_t grow = kvb + lo + r;
                         st16(krow(off + r) + 8 * c, ld16(kg + grow * tp.sk_t + 8 * c));
                         st16(vrow(off + r) + 8 * c, ld16(vg + grow * tp.sv_t + 8 * c));
+                        if constexpr (DBG) {
+                            if (c == 0) dbg_slot[off + r] = lo + r;
+                        }
                     }
                     off += sz;
                 }
@@ -541,6 +560,9 @@ __global__ __launch_bounds__(kPrefixThreads) __attribute__((amdgpu_waves_per_eu(
             for (int b = 0; b < kQB; ++b) {
                 float sc = qk4<T, NCH>(qf4[b], k0[b]) * tp.scale_log2;
                 fold_scores<T, NCH, 1>(&sc, &v0[b], mw[b], lw[b], acc[b]);
+                if constexpr (DBG) {
+                    if (dbg[b]) dbg[b][0] = tokb[b];
+                }
                 prev[b] = tokb[b];
                 cur[b] = heap_parent(tokb[b], tp.bdiv);
             }
@@ -560,6 +582,9 @@ __global__ __launch_bounds__(kPrefixThreads) __attribute__((amdgpu_waves_per_eu(
                     float sc = qk4<T, NCH>(qf4[b], kk) * tp.scale_log2;
                     sc = cur[b] != prev[b] ? sc : -INFINITY;  // the root's self-loop is not a step
                     fold_scores<T, NCH, 1>(&sc, vv, mw[b], lw[b], acc[b]);
+                    if constexpr (DBG) {
+                        if (dbg[b]) dbg[b][t] = cur[b] != prev[b] ? dbg_slot[slot] : -1;
+                    }
                     prev[b] = cur[b];
                     cur[b] = heap_parent(cur[b], tp.bdiv);
                 }
@@ -570,8 +595,8 @@ __global__ __launch_bounds__(kPrefixThreads) __attribute__((amdgpu_waves_per_eu(
             // D = 64 up (two full chunks in flight spill registers there)
             constexpr int CH1 = 8 / NCH;
             constexpr int CHW = D >= 64 ? CH1 / 2 : CH1;
-            using W = Walk4<T, D, WALK, KV_PACKED, CHW, BATCH>;
-            W w0(tp, seq, s0, n, tokb[0], kvh, j), w1(tp, seq, s0, n, tokb[1], kvh, j);
+            using W = Walk4<T, D, WALK, KV_PACKED, CHW, BATCH, DBG>;
+            W w0(tp, seq, s0, n, tokb[0], kvh, j, nullptr, dbg[0]), w1(tp, seq, s0, n, tokb[1], kvh, j, nullptr, dbg[1]);
             w0.issue();
             w1.issue();
             w0.fold(qf4[0], mw[0], lw[0], acc[0]);
@@ -585,10 +610,63 @@ __global__ __launch_bounds__(kPrefixThreads) __attribute__((amdgpu_waves_per_eu(
                 if (a1) w1.fold(qf4[1], mw[1], lw[1], acc[1]);
             }
         }
+        }
 #pragma unroll
         for (int b = 0; b < kQB; ++b)
             if (vb[b]) write_out4<T, D, LSE, BATCH>(tp, seq, qrb[b], hb[b], j, mw[b], lw[b], acc[b]);
     }
+}
+
+// ---------------------------------------------------------------------------
+// Split merge of the prefix-only pass: 4 lanes per (token, q head) fold the
+// splits' partial states and store the normalised output (+ LSE).
+// ---------------------------------------------------------------------------
+template <typename T, int D, bool LSE, bool BATCH>
+__global__ __launch_bounds__(kPrefixThreads) void prefix_merge_kernel(TreeParams p) {
+    constexpr int SLOTS = kPrefixThreads / 4;
+    const int j = threadIdx.x & 3;
+    const int64_t slot = (int64_t)blockIdx.x * SLOTS + (threadIdx.x >> 2);
+    const int h = (int)(slot % p.Hq);
+    const int64_t rest = slot / p.Hq;
+    const int tok = (int)(rest % p.max_seqlen);
+    const int seq = (int)(rest / p.max_seqlen);
+    if (seq >= p.B) return;
+    int32_t start, n;
+    if (!seq_bounds<BATCH>(p, seq, start, n)) return;
+    if (tok >= n) return;
+    const int64_t qrow = (int64_t)start + tok;
+    float m, l, acc[8 * (D / 32)];
+    load_partial_state4<D>(p, qrow, h, j, m, l, acc);
+    write_out4<T, D, LSE, BATCH>(p, seq, qrow, h, j, m, l, acc);
+}
+
+template <typename T, int D, bool BATCH>
+static int launch_prefix_merge(const TreeParams& p, hipStream_t st) {
+    constexpr int SLOTS = kPrefixThreads / 4;
+    const int64_t blocks = ((int64_t)p.B * p.max_seqlen * p.Hq + SLOTS - 1) / SLOTS;
+    if (blocks >= (int64_t(1) << 31)) {
+        set_error("merge grid too large (%lld blocks)", (long long)blocks);
+        return QATTN_ERR_ARG;
+    }
+    if (p.lse)
+        hipLaunchKernelGGL((prefix_merge_kernel<T, D, true, BATCH>), dim3((unsigned)blocks), dim3(kPrefixThreads), 0,
+                           st, p);
+    else
+        hipLaunchKernelGGL((prefix_merge_kernel<T, D, false, BATCH>), dim3((unsigned)blocks), dim3(kPrefixThreads),
+                           0, st, p);
+    return launch_status("prefix_merge_kernel");
+}
+
+template <typename T>
+static int run_prefix_merge(const TreeParams& p, int head_dim, hipStream_t st) {
+    if (!p.cu) {
+        return head_dim == 32   ? launch_prefix_merge<T, 32, true>(p, st)
+               : head_dim == 64 ? launch_prefix_merge<T, 64, true>(p, st)
+                                : launch_prefix_merge<T, 128, true>(p, st);
+    }
+    return head_dim == 32   ? launch_prefix_merge<T, 32, false>(p, st)
+           : head_dim == 64 ? launch_prefix_merge<T, 64, false>(p, st)
+                            : launch_prefix_merge<T, 128, false>(p, st);
 }
 
 // ---------------------------------------------------------------------------
@@ -630,8 +708,24 @@ template <typename T, int D, bool BATCH>
 static void launch_prefix_b(const PrefixParams& pp, const TreeParams& tp, bool fused, int walk, dim3 g,
                             hipStream_t st) {
     const dim3 b(kPrefixThreads);
+    if constexpr (T::kCode == QATTN_DTYPE_F16 && !BATCH) {
+        // walk export (the caller has checked: fp16, packed, no LSE)
+        if (fused && tp.dbg_walk && walk == WALK_HEAP) {
+            hipLaunchKernelGGL((prefix_attn_kernel<F16, D, true, false, WALK_HEAP, false, true>), g, b, 0, st, pp, tp);
+            return;
+        }
+        if (fused && tp.dbg_walk && walk == WALK_PARENTS) {
+            hipLaunchKernelGGL((prefix_attn_kernel<F16, D, true, false, WALK_PARENTS, false, true>), g, b, 0, st, pp,
+                               tp);
+            return;
+        }
+    }
     if (!fused)
         hipLaunchKernelGGL((prefix_attn_kernel<T, D, false, false, WALK_HEAP, BATCH>), g, b, 0, st, pp, tp);
+    else if (walk == WALK_NONE && tp.lse)
+        hipLaunchKernelGGL((prefix_attn_kernel<T, D, true, true, WALK_NONE, BATCH>), g, b, 0, st, pp, tp);
+    else if (walk == WALK_NONE)
+        hipLaunchKernelGGL((prefix_attn_kernel<T, D, true, false, WALK_NONE, BATCH>), g, b, 0, st, pp, tp);
     else if (walk == WALK_PARENTS && tp.lse)
         hipLaunchKernelGGL((prefix_attn_kernel<T, D, true, true, WALK_PARENTS, BATCH>), g, b, 0, st, pp, tp);
     else if (walk == WALK_PARENTS)
@@ -669,8 +763,9 @@ struct BatchView {
     int32_t par_stride;
 };
 
-// Shared body of the prefix entry points: parents null walks the heap tree of
-// branching_factor, else the explicit parent array; bv null is the cu-packed
+// Shared body of the prefix entry points.  walk: WALK_HEAP walks the heap
+// tree of branching_factor, WALK_PARENTS the explicit parent array,
+// WALK_NONE attends the prefix only (k, v unused); bv null is the cu-packed
 // layout, else a uniform batch (cu_seqlens unused).
 static int prefix_tree_impl(const void* q, const int64_t q_stride[3], const void* k, const int64_t k_stride[3],
                             const void* v, const int64_t v_stride[3], const void* k_prefix,
@@ -681,7 +776,7 @@ static int prefix_tree_impl(const void* q, const int64_t q_stride[3], const void
                             int64_t tree_row0, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
                             int32_t branching_factor, int32_t max_depth, float scale, int32_t dtype,
                             void* workspace, int64_t workspace_size, int32_t num_splits, void* stream,
-                            const BatchView* bv) {
+                            const BatchView* bv, int walk) {
     int rc = check_common(dtype, head_dim, batch, max_seqlen, total_tokens, num_q_heads, num_kv_heads, max_depth);
     if (rc) return rc;
     if (!(scale > 0.f)) {
@@ -693,10 +788,17 @@ static int prefix_tree_impl(const void* q, const int64_t q_stride[3], const void
                   (long long)tree_row0);
         return QATTN_ERR_ARG;
     }
+    if (walk == WALK_NONE && prefix_len < 1) {
+        set_error("prefix-only attention needs prefix_len >= 1 (got %d)", prefix_len);
+        return QATTN_ERR_ARG;
+    }
     if (batch == 0 || max_seqlen == 0 || total_tokens == 0) return QATTN_OK;
+    // (the prefix-only pass reads no tree rows: q stands in for k and v)
+    const bool tree = walk != WALK_NONE;
     TreeParams tp;
-    rc = fill_tree_params(tp, q, q_stride, k, k_stride, v, v_stride, o, o_stride, lse, lse_stride, cu_seqlens, batch,
-                          max_seqlen, total_tokens, num_q_heads, num_kv_heads, branching_factor, max_depth, scale,
+    rc = fill_tree_params(tp, q, q_stride, tree ? k : q, tree ? k_stride : q_stride, tree ? v : q,
+                          tree ? v_stride : q_stride, o, o_stride, lse, lse_stride, cu_seqlens, batch, max_seqlen,
+                          total_tokens, num_q_heads, num_kv_heads, branching_factor, max_depth, scale,
                           bv != nullptr);
     if (rc) return rc;
     if (bv) {
@@ -706,14 +808,13 @@ static int prefix_tree_impl(const void* q, const int64_t q_stride[3], const void
         tp.slse_b = bv->lse_b;
         tp.par_stride = bv->par_stride;
     }
-    if (!row_aligned(k, k_stride, 2) || !row_aligned(v, v_stride, 2)) {
+    if (tree && (!row_aligned(k, k_stride, 2) || !row_aligned(v, v_stride, 2))) {
         set_error("k/v rows must be 16-byte aligned with stride_dim 1");
         return QATTN_ERR_LAYOUT;
     }
     tp.kv_seq_stride = tree_seq_stride;
     tp.kv_row0 = tree_row0;
     tp.parents = parents;
-    const int walk = parents ? WALK_PARENTS : WALK_HEAP;
     hipStream_t st = (hipStream_t)stream;
     if (prefix_len == 0) return run_tree(tp, dtype, head_dim, walk, KV_PACKED, false, QATTN_ALGO_AUTO, st);
 
@@ -747,6 +848,10 @@ static int prefix_tree_impl(const void* q, const int64_t q_stride[3], const void
         return QATTN_ERR_ARG;
     }
     const bool fused = splits == 1;
+    if (tp.dbg_walk && (dtype != QATTN_DTYPE_F16 || lse || !tp.cu)) {
+        set_error("the walk export runs fp16 calls over packed cu_seqlens without LSE");
+        return QATTN_ERR_ARG;
+    }
     const int64_t plane = total_tokens * num_q_heads;
     PrefixParams pp{};
     pp.q = q;
@@ -794,70 +899,21 @@ static int prefix_tree_impl(const void* q, const int64_t q_stride[3], const void
     tp.part_l = pp.part_l;
     tp.part_acc = pp.part_acc;
     tp.n_split = splits;
+    if (!tree)
+        return dtype == QATTN_DTYPE_F16 ? run_prefix_merge<F16>(tp, head_dim, st)
+                                        : run_prefix_merge<BF16>(tp, head_dim, st);
     return run_tree(tp, dtype, head_dim, walk, KV_PACKED, true, QATTN_ALGO_AUTO, st);
 }
 
-
-extern "C" {
-
-int64_t qattn_prefix_workspace_bytes(int32_t batch, int32_t max_seqlen, int64_t total_tokens, int32_t num_q_heads,
-                                     int32_t num_kv_heads, int32_t head_dim, int32_t prefix_len, int32_t num_splits) {
-    if (batch <= 0 || max_seqlen <= 0 || total_tokens <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 ||
-        num_q_heads % num_kv_heads || prefix_len <= 0)
-        return 0;
-    int bps = 0;
-    const int splits =
-        prefix_splits(units_per_split(batch, num_kv_heads, max_seqlen, num_q_heads / num_kv_heads), prefix_len,
-                      num_splits, bps);
-    return workspace_bytes(total_tokens, num_q_heads, head_dim, splits);
-}
-
-int qattn_prefix_tree_fwd(const void* q, const int64_t q_stride[3], const void* k, const int64_t k_stride[3],
-                          const void* v, const int64_t v_stride[3], const void* k_prefix,
-                          const int64_t kp_stride[3], const void* v_prefix, const int64_t vp_stride[3],
-                          int32_t prefix_len, void* o, const int64_t o_stride[3], float* lse,
-                          const int64_t lse_stride[2], const int32_t* cu_seqlens, int32_t batch,
-                          int32_t max_seqlen, int64_t total_tokens, int64_t tree_seq_stride, int64_t tree_row0,
-                          int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, int32_t branching_factor,
-                          int32_t max_depth, float scale, int32_t dtype, void* workspace, int64_t workspace_size,
-                          int32_t num_splits, void* stream) {
-    clear_error();
-    return prefix_tree_impl(q, q_stride, k, k_stride, v, v_stride, k_prefix, kp_stride, v_prefix, vp_stride,
-                            prefix_len, o, o_stride, lse, lse_stride, cu_seqlens, nullptr, batch, max_seqlen,
-                            total_tokens, tree_seq_stride, tree_row0, num_q_heads, num_kv_heads, head_dim,
-                            branching_factor, max_depth, scale, dtype, workspace, workspace_size, num_splits, stream,
-                            nullptr);
-}
-
-int qattn_prefix_tree_parents_fwd(const void* q, const int64_t q_stride[3], const void* k,
-                                  const int64_t k_stride[3], const void* v, const int64_t v_stride[3],
-                                  const void* k_prefix, const int64_t kp_stride[3], const void* v_prefix,
-                                  const int64_t vp_stride[3], int32_t prefix_len, void* o,
-                                  const int64_t o_stride[3], float* lse, const int64_t lse_stride[2],
-                                  const int32_t* cu_seqlens, const int32_t* parents, int32_t batch,
-                                  int32_t max_seqlen, int64_t total_tokens, int64_t tree_seq_stride,
-                                  int64_t tree_row0, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
-                                  int32_t max_depth, float scale, int32_t dtype, void* workspace,
-                                  int64_t workspace_size, int32_t num_splits, void* stream) {
-    clear_error();
-    if (!parents && batch > 0 && max_seqlen > 0 && total_tokens > 0) {
-        set_error("parents is null");
-        return QATTN_ERR_ARG;
-    }
-    return prefix_tree_impl(q, q_stride, k, k_stride, v, v_stride, k_prefix, kp_stride, v_prefix, vp_stride,
-                            prefix_len, o, o_stride, lse, lse_stride, cu_seqlens, parents, batch, max_seqlen,
-                            total_tokens, tree_seq_stride, tree_row0, num_q_heads, num_kv_heads, head_dim, 1,
-                            max_depth, scale, dtype, workspace, workspace_size, num_splits, stream, nullptr);
-}
-
-int qattn_ragged_tree_attn_fwd(const void* q, const int64_t q_stride[4], const void* k, const int64_t k_stride[4],
-                               const void* v, const int64_t v_stride[4], void* o, const int64_t o_stride[4],
-                               float* lse, const int64_t lse_stride[3], const int32_t* parents,
-                               int64_t parents_stride, int32_t batch, int32_t num_tree, int32_t num_prefix,
-                               int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
-                               int32_t branching_factor, int32_t max_depth, float scale, int32_t dtype,
-                               void* workspace, int64_t workspace_size, int32_t num_splits, void* stream) {
-    clear_error();
+// The [B, H, N, D] view entry (qattn_ragged_tree_attn_fwd and its
+// allocation-free variant): strides to the packed form, then prefix_tree_impl.
+static int ragged_tree_attn_impl(const void* q, const int64_t q_stride[4], const void* k, const int64_t k_stride[4],
+                                 const void* v, const int64_t v_stride[4], void* o, const int64_t o_stride[4],
+                                 float* lse, const int64_t lse_stride[3], const int32_t* parents,
+                                 int64_t parents_stride, int32_t batch, int32_t num_tree, int32_t num_prefix,
+                                 int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                                 int32_t branching_factor, int32_t max_depth, float scale, int32_t dtype,
+                                 void* workspace, int64_t workspace_size, int32_t num_splits, void* stream) {
     if (!q_stride || !k_stride || !v_stride || !o_stride || (lse && !lse_stride)) {
         set_error("null stride array");
         return QATTN_ERR_ARG;
@@ -908,7 +964,98 @@ int qattn_ragged_tree_attn_fwd(const void* q, const int64_t q_stride[4], const v
     return prefix_tree_impl(q, q3, k, k3, v, v3, k, kp3, v, vp3, num_prefix, o, o3, lse, lse ? lse2 : nullptr,
                             nullptr, parents, batch, num_tree, total, seq_rows, num_prefix, num_q_heads,
                             num_kv_heads, head_dim, parents ? 1 : branching_factor, max_depth, scale, dtype,
-                            workspace, workspace_size, num_splits, stream, &bv);
+                            workspace, workspace_size, num_splits, stream, &bv,
+                            parents ? WALK_PARENTS : WALK_HEAP);
+}
+
+extern "C" {
+
+int qattn_init(void) {
+    clear_error();
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess) {
+        set_error("hipGetDevice failed");
+        return QATTN_ERR_HIP;
+    }
+    return sched_init(dev);
+}
+
+int64_t qattn_prefix_workspace_bytes(int32_t batch, int32_t max_seqlen, int64_t total_tokens, int32_t num_q_heads,
+                                     int32_t num_kv_heads, int32_t head_dim, int32_t prefix_len, int32_t num_splits) {
+    if (batch <= 0 || max_seqlen <= 0 || total_tokens <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 ||
+        num_q_heads % num_kv_heads || prefix_len <= 0)
+        return 0;
+    int bps = 0;
+    const int splits =
+        prefix_splits(units_per_split(batch, num_kv_heads, max_seqlen, num_q_heads / num_kv_heads), prefix_len,
+                      num_splits, bps);
+    return workspace_bytes(total_tokens, num_q_heads, head_dim, splits);
+}
+
+int qattn_prefix_tree_fwd(const void* q, const int64_t q_stride[3], const void* k, const int64_t k_stride[3],
+                          const void* v, const int64_t v_stride[3], const void* k_prefix,
+                          const int64_t kp_stride[3], const void* v_prefix, const int64_t vp_stride[3],
+                          int32_t prefix_len, void* o, const int64_t o_stride[3], float* lse,
+                          const int64_t lse_stride[2], const int32_t* cu_seqlens, int32_t batch,
+                          int32_t max_seqlen, int64_t total_tokens, int64_t tree_seq_stride, int64_t tree_row0,
+                          int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, int32_t branching_factor,
+                          int32_t max_depth, float scale, int32_t dtype, void* workspace, int64_t workspace_size,
+                          int32_t num_splits, void* stream) {
+    clear_error();
+    return prefix_tree_impl(q, q_stride, k, k_stride, v, v_stride, k_prefix, kp_stride, v_prefix, vp_stride,
+                            prefix_len, o, o_stride, lse, lse_stride, cu_seqlens, nullptr, batch, max_seqlen,
+                            total_tokens, tree_seq_stride, tree_row0, num_q_heads, num_kv_heads, head_dim,
+                            branching_factor, max_depth, scale, dtype, workspace, workspace_size, num_splits, stream,
+                            nullptr, WALK_HEAP);
+}
+
+int qattn_prefix_tree_parents_fwd(const void* q, const int64_t q_stride[3], const void* k,
+                                  const int64_t k_stride[3], const void* v, const int64_t v_stride[3],
+                                  const void* k_prefix, const int64_t kp_stride[3], const void* v_prefix,
+                                  const int64_t vp_stride[3], int32_t prefix_len, void* o,
+                                  const int64_t o_stride[3], float* lse, const int64_t lse_stride[2],
+                                  const int32_t* cu_seqlens, const int32_t* parents, int32_t batch,
+                                  int32_t max_seqlen, int64_t total_tokens, int64_t tree_seq_stride,
+                                  int64_t tree_row0, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                                  int32_t max_depth, float scale, int32_t dtype, void* workspace,
+                                  int64_t workspace_size, int32_t num_splits, void* stream) {
+    clear_error();
+    if (!parents && batch > 0 && max_seqlen > 0 && total_tokens > 0) {
+        set_error("parents is null");
+        return QATTN_ERR_ARG;
+    }
+    return prefix_tree_impl(q, q_stride, k, k_stride, v, v_stride, k_prefix, kp_stride, v_prefix, vp_stride,
+                            prefix_len, o, o_stride, lse, lse_stride, cu_seqlens, parents, batch, max_seqlen,
+                            total_tokens, tree_seq_stride, tree_row0, num_q_heads, num_kv_heads, head_dim, 1,
+                            max_depth, scale, dtype, workspace, workspace_size, num_splits, stream, nullptr,
+                            WALK_PARENTS);
+}
+
+int qattn_prefix_fwd(const void* q, const int64_t q_stride[3], const void* k_prefix, const int64_t kp_stride[3],
+                     const void* v_prefix, const int64_t vp_stride[3], int32_t prefix_len, void* o,
+                     const int64_t o_stride[3], float* lse, const int64_t lse_stride[2],
+                     const int32_t* cu_seqlens, int32_t batch, int32_t max_seqlen, int64_t total_tokens,
+                     int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, float scale, int32_t dtype,
+                     void* workspace, int64_t workspace_size, int32_t num_splits, void* stream) {
+    clear_error();
+    return prefix_tree_impl(q, q_stride, nullptr, nullptr, nullptr, nullptr, k_prefix, kp_stride, v_prefix,
+                            vp_stride, prefix_len, o, o_stride, lse, lse_stride, cu_seqlens, nullptr, batch,
+                            max_seqlen, total_tokens, 0, 0, num_q_heads, num_kv_heads, head_dim, 1, 0, scale, dtype,
+                            workspace, workspace_size, num_splits, stream, nullptr, WALK_NONE);
+}
+
+int qattn_ragged_tree_attn_fwd(const void* q, const int64_t q_stride[4], const void* k, const int64_t k_stride[4],
+                               const void* v, const int64_t v_stride[4], void* o, const int64_t o_stride[4],
+                               float* lse, const int64_t lse_stride[3], const int32_t* parents,
+                               int64_t parents_stride, int32_t batch, int32_t num_tree, int32_t num_prefix,
+                               int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                               int32_t branching_factor, int32_t max_depth, float scale, int32_t dtype,
+                               void* workspace, int64_t workspace_size, int32_t num_splits, void* stream) {
+    clear_error();
+    return ragged_tree_attn_impl(q, q_stride, k, k_stride, v, v_stride, o, o_stride, lse, lse_stride, parents,
+                                 parents_stride, batch, num_tree, num_prefix, num_q_heads, num_kv_heads, head_dim,
+                                 branching_factor, max_depth, scale, dtype, workspace, workspace_size, num_splits,
+                                 stream);
 }
 
 }  // extern "C"

@@ -86,6 +86,10 @@ struct TreeParams {
     // by every sequence; packed: at the sequence's first row).
     int64_t sq_b, so_b, slse_b;
     int32_t par_stride;
+    // Walk export (qattn_debug_walk; null in normal calls): int32
+    // [total_tokens][Hq][max_depth + 1], entry i = the node a query attended
+    // at walk step i, or -1.  Only the kernels' debug instantiations read it.
+    int32_t* dbg_walk;
 };
 
 // Subtree tiling of a heap-indexed tree (levels of the BFS order).
@@ -113,11 +117,12 @@ struct SubtreePlan {
 // gsize, gsize+1, ...; sched[g * kSchedStride + 1] counts the workgroups that
 // are done, and the last one resets both to zero), without it workgroup j
 // takes j, j + gsize, ...  Counter pairs of one launch lie kSchedStride words
-// (1 KB) apart, so no two groups share a cache line: atomics on one line are
+// (2 KB) apart, so no two groups share a cache line: atomics on one line are
 // serialised, and 4000-8000 requests per launch on a single line made the
-// kernel 10-20% slower.  The words in between hold other launches' pairs.
-constexpr int kSchedGroups = 2048;
-constexpr int kSchedSlots = 128;                // launches with counters of their own
+// kernel 10-20% slower.  The words in between hold other slots' pairs.  A
+// launch has at most 3 workgroups per CU, so at most 768 groups on 256 CUs.
+constexpr int kSchedGroups = 1024;
+constexpr int kSchedSlots = 256;                // launches with counters of their own
 constexpr int kSchedStride = 2 * kSchedSlots;   // words between groups of one launch
 
 struct StreamArgs {
@@ -137,6 +142,9 @@ void stream_tile_caps(int head_dim, int* kv_rows, int* q_rows);
 int stream_max_batch();
 int launch_stream(const TreeParams& p, const SubtreePlan& plan, int dtype, int head_dim, bool pstate,
                   hipStream_t st);
+// qattn_init's part for the subtree kernel: the device address of the
+// current device's counter pool, zeroed (synchronously, on a private stream).
+int sched_init(int dev);
 
 void set_error(const char* fmt, ...);
 void clear_error();

@@ -63,6 +63,9 @@ struct StreamGeom {
     static constexpr int ND = D / 16;                 // 16-row d-tiles of O^T
     static constexpr size_t LDS_BYTES = ((size_t)(KV_ROWS + Q_ROWS + V_ROWS) * PITCH) * 2 +
                                         (size_t)Q_ROWS * sizeof(QueryEntry) + kCuCache * 4 + 16;
+    // walk export only: the staged row maps (node of each K/V row, token and
+    // head offset of each Q row)
+    static constexpr size_t DBG_BYTES = (size_t)(KV_ROWS + Q_ROWS) * 4;
 };
 
 // Per-tile state.  Scalars are wave-uniform; first/cnt/off/qb are per lane,
@@ -323,12 +326,25 @@ __device__ __forceinline__ void tile_issue(const TreeParams& p, const TileMeta& 
 // Write the staged tile to LDS (K, V and Q rows at the padded pitch).  V rows
 // past the tile's last row keep the previous tile's (finite) values or the
 // zeros written at kernel start; P = 0 multiplies them.
-template <int D>
+template <int D, bool DBG = false>
 __device__ __forceinline__ void tile_store(const TileMeta& t, uint16_t* Ks, uint16_t* Vs, uint16_t* Qs,
-                                           const Stage<D>& sg) {
+                                           const Stage<D>& sg, const RowMap<D>& rm, int32_t* dbg_row,
+                                           int32_t* dbg_q) {
     using Geo = StreamGeom<D>;
     const int tid = threadIdx.x;
     const int rsub = tid / Geo::CPR, c = tid % Geo::CPR;
+    if constexpr (DBG) {
+        // the map the loads of this tile were issued with (row r of LDS holds
+        // node dbg_row[r] of the sequence; Q row q holds token/head dbg_q[q])
+        if (c == 0) {
+#pragma unroll
+            for (int ps = 0; ps < Geo::PASSES; ++ps) {
+                const int r = ps * Geo::RPP + rsub;
+                dbg_row[r] = r < t.rows ? rm.kvrow[ps] : -1;
+                dbg_q[r] = r < t.nq ? rm.qrow[ps] : -1;
+            }
+        }
+    }
 #pragma unroll
     for (int ps = 0; ps < Geo::PASSES; ++ps) {
         if (ps * Geo::RPP >= t.rows) break;
@@ -395,6 +411,47 @@ __device__ __forceinline__ void build_query_table(const TreeParams& p, const Div
     }
 }
 
+// Walk export: the ancestor set each query of the tile attends, read back
+// from what the compute uses -- its row mask in the query table, each set bit
+// mapped to the node whose K/V row the loads put in that LDS row -- and
+// written as [token][q head][step] (step = the query's depth minus the
+// row's).  A bit on a row without a node, two rows at one step, or a Q row
+// staged from another token/head than the table says marks the entry -2 at
+// step 0.
+__device__ __forceinline__ void dbg_walk_export(const TreeParams& p, const TileMeta& t, const QueryEntry* qt,
+                                                const int32_t* dbg_row, const int32_t* dbg_q) {
+    const int S1 = p.max_depth + 1;
+    auto depth = [&](int32_t x) {
+        int dd = 0;
+        while (x > 0) {
+            x = heap_parent(x, p.bdiv);
+            ++dd;
+        }
+        return dd;
+    };
+    for (int q = threadIdx.x; q < t.nq; q += kStThreads) {
+        const QueryEntry qe = qt[q];
+        const uint64_t mask = ((uint64_t)qe.mask_hi << 32) | qe.mask_lo;
+        bool bad = dbg_q[q] != ((qe.node << 8) | qe.hoff);
+        int32_t* out = p.dbg_walk + (((int64_t)t.start + qe.node) * p.Hq + t.kvh * p.group + qe.hoff) * S1;
+        for (int i = 0; i < S1; ++i) out[i] = -1;
+        const int dq = depth(qe.node);
+        uint64_t filled = 0;
+        for (int r = 0; r < 64; ++r) {
+            if (!((mask >> r) & 1u)) continue;
+            const int32_t node = dbg_row[r];
+            const int step = node >= 0 ? dq - depth(node) : -1;
+            if (node < 0 || step < 0 || step >= S1 || ((filled >> step) & 1u)) {
+                bad = true;
+                continue;
+            }
+            filled |= uint64_t(1) << step;
+            out[step] = node;
+        }
+        if (bad) out[0] = -2;
+    }
+}
+
 // One wave: attention of 16 queries (query block qb) of the tile held in LDS.
 template <typename T, int D, bool LSE, bool PSTATE, bool BATCH>
 __device__ __forceinline__ void block_compute(const TreeParams& p, const TileMeta& t, int qb, const uint16_t* Ks,
@@ -442,20 +499,22 @@ __device__ __forceinline__ void block_compute(const TreeParams& p, const TileMet
 
     __builtin_amdgcn_sched_barrier(0);  // keep the PV operand reads below the softmax
     // ---- masked softmax per query column ----
+    // Scores are scaled before the mask and the max, so any finite scale
+    // works (zero or negative included).
+    const float c = p.scale_log2;
     float mx = -INFINITY;
 #pragma unroll
     for (int kt = 0; kt < KT; ++kt) {
         const uint32_t bits = (uint32_t)(mask >> (16 * kt + 4 * i4)) & 15u;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const float s = ((bits >> r) & 1u) ? sacc[kt][r] : -INFINITY;
+            const float s = ((bits >> r) & 1u) ? sacc[kt][r] * c : -INFINITY;
             sacc[kt][r] = s;
             mx = fmaxf(mx, s);
         }
     }
     mx = col4_max(mx);
-    const float c = p.scale_log2;
-    float mref = (mx == -INFINITY) ? 0.f : mx * c;  // a query with no row (invalid column)
+    float mref = (mx == -INFINITY) ? 0.f : mx;  // a query with no row (invalid column)
     // Split-K prefix partial states (flash-decoding merge): the reference
     // becomes max(tree max, prefix max) and the accumulators start from the
     // prefix states weighted by 2^(m_s - reference), one split at a time.
@@ -495,7 +554,7 @@ __device__ __forceinline__ void block_compute(const TreeParams& p, const TileMet
     for (int kt = 0; kt < KT; ++kt) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const float e = fast_exp2(__builtin_fmaf(sacc[kt][r], c, -mc));  // -inf -> 0
+            const float e = fast_exp2(sacc[kt][r] - mc);  // -inf -> 0
             sacc[kt][r] = e;
             ls += e;
         }
@@ -605,7 +664,9 @@ __device__ __forceinline__ uint32_t sched_grab(uint32_t* ctr) {
 // so the next launch finds them at zero.
 // BATCH: a uniform batch (null cu, per-sequence q/o/lse offsets); the packed
 // layout compiles without that addressing.
-template <typename T, int D, bool LSE, bool PSTATE, bool BATCH>
+// DBG: the walk-export instantiation (qattn_debug_walk), which also writes
+// every query's attended ancestor set to p.dbg_walk.
+template <typename T, int D, bool LSE, bool PSTATE, bool BATCH, bool DBG = false>
 __global__ __launch_bounds__(kStThreads)
 __attribute__((amdgpu_waves_per_eu(3, 3))) void tree_stream_kernel(
     TreeParams p, SubtreePlan plan, StreamArgs sa) {
@@ -617,6 +678,8 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void tree_stream_kernel(
     QueryEntry* qtab = reinterpret_cast<QueryEntry*>(Vs + Geo::V_ROWS * Geo::PITCH);
     int32_t* cuc = reinterpret_cast<int32_t*>(qtab + Geo::Q_ROWS);
     int32_t* next_slot = cuc + kCuCache;  // the workgroup's next item, written by thread 0
+    int32_t* dbg_row = next_slot + 4;     // (DBG only: LDS_BYTES + DBG_BYTES are allocated)
+    int32_t* dbg_q = dbg_row + Geo::KV_ROWS;
     const Divider gdiv = sa.gdiv;
 
     const int grp = divide((int)blockIdx.x, sa.ngroups);
@@ -688,7 +751,7 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void tree_stream_kernel(
         __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
         if (first && threadIdx.x <= p.B) cuc[threadIdx.x] = cu_mine;
         first = false;
-        if (cur.valid) tile_store<D>(cur, Ks, Vs, Qs, sg);
+        if (cur.valid) tile_store<D, DBG>(cur, Ks, Vs, Qs, sg, rm, dbg_row, dbg_q);
         if (leader) *next_slot = dyn ? sa.gsize + (int)ans : k + sa.gsize;
         __syncthreads();
         const int kn = __builtin_amdgcn_readfirstlane(*next_slot);
@@ -712,6 +775,7 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void tree_stream_kernel(
                 tab_n = cur.n;
                 __syncthreads();
             }
+            if constexpr (DBG) dbg_walk_export(p, cur, qtab, dbg_row, dbg_q);
             tile_compute<T, D, LSE, PSTATE, BATCH>(p, cur, Ks, Vs, Qs, qtab);
         }
         __syncthreads();
@@ -728,50 +792,88 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void tree_stream_kernel(
     }
 }
 
-// Scheduler counters (StreamArgs::sched): per device one allocation of
-// kSchedGroups * kSchedStride words, zeroed once, holding kSchedSlots counter
-// slots (a slot: one counter pair per group, kSchedStride words apart).  Every
-// launch leaves its slot at zero when it completes.  Eager launches take the
-// first kSchedRing slots in turn, so launches that overlap in time use
-// different slots unless more than kSchedRing of them are in flight at once.
-// A launch recorded into a graph keeps one of the other slots for every
-// replay (replays of one graph run in stream order); when those run out, or
-// when the first launch on a device is being recorded (no allocation then),
-// the kernel uses the static schedule.
-constexpr int kSchedRing = 32, kSchedMaxDev = 64;
+// Scheduler counters (StreamArgs::sched): a static device array of
+// kSchedGroups * kSchedStride words per device (each GPU holds its own copy),
+// zeroed by qattn_init, holding kSchedSlots counter slots (a slot: one counter
+// pair per group, kSchedStride words apart).  Every launch leaves its slot at
+// zero when it completes.
+//
+// A slot may only serve launches that cannot overlap in time:
+//  * an eager launch takes the slot of its stream (launches on one stream run
+//    in order; the first kSchedStreamSlots streams seen on a device get one
+//    each, later streams run the static schedule);
+//  * a launch recorded into a graph keeps a slot of its own for every replay
+//    (replays of one graph executable run in order); when the recorded slots
+//    run out the launch is recorded with the static schedule.
+// Before qattn_init has run on a device every launch uses the static schedule
+// (same results, slower): the library never allocates, zeroes or
+// synchronises behind a call.
+constexpr int kSchedStreamSlots = 64, kSchedMaxDev = 64;
+static __device__ __align__(256) uint32_t sched_pool[kSchedGroups * kSchedStride];
+
+namespace {
+struct SchedDevice {
+    uint32_t* pool = nullptr;  // device address of this device's sched_pool
+    hipStream_t streams[kSchedStreamSlots] = {};
+    int n_streams = 0, captured_next = 0;
+};
+std::mutex g_sched_mu;
+SchedDevice g_sched[kSchedMaxDev];
+}  // namespace
+
+int sched_init(int dev) {
+    if (dev < 0 || dev >= kSchedMaxDev) {
+        set_error("device %d beyond the %d devices the library tracks", dev, kSchedMaxDev);
+        return QATTN_ERR_ARG;
+    }
+    std::lock_guard<std::mutex> lock(g_sched_mu);
+    if (g_sched[dev].pool) return QATTN_OK;
+    void* ptr = nullptr;
+    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(sched_pool)) != hipSuccess || !ptr) {
+        set_error("hipGetSymbolAddress(sched_pool) failed on device %d", dev);
+        return QATTN_ERR_HIP;
+    }
+    // zero the counters on a private stream (not the caller's, not captured)
+    hipStream_t s = nullptr;
+    if (hipStreamCreateWithFlags(&s, hipStreamNonBlocking) != hipSuccess) {
+        set_error("cannot create the init stream on device %d", dev);
+        return QATTN_ERR_HIP;
+    }
+    const hipError_t e1 = hipMemsetAsync(ptr, 0, sizeof(sched_pool), s);
+    const hipError_t e2 = hipStreamSynchronize(s);
+    (void)hipStreamDestroy(s);
+    if (e1 != hipSuccess || e2 != hipSuccess) {
+        set_error("zeroing the schedule counters failed on device %d", dev);
+        return QATTN_ERR_HIP;
+    }
+    g_sched[dev].pool = (uint32_t*)ptr;
+    return QATTN_OK;
+}
 
 static uint32_t* sched_counters(int dev, hipStream_t st) {
-    static std::mutex mu;
-    static uint32_t* pool[kSchedMaxDev] = {};
-    static int ring_next[kSchedMaxDev] = {}, captured_next[kSchedMaxDev] = {};
     if (dev < 0 || dev >= kSchedMaxDev) return nullptr;
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     if (hipStreamIsCapturing(st, &cs) != hipSuccess) return nullptr;
-    const bool capturing = cs != hipStreamCaptureStatusNone;
-    std::lock_guard<std::mutex> lock(mu);
-    if (!pool[dev]) {
-        if (capturing) return nullptr;
-        const size_t bytes = (size_t)kSchedGroups * kSchedStride * sizeof(uint32_t);
-        void* ptr = nullptr;
-        if (hipMalloc(&ptr, bytes) != hipSuccess) return nullptr;
-        if (hipMemset(ptr, 0, bytes) != hipSuccess) {
-            (void)hipFree(ptr);
-            return nullptr;
-        }
-        pool[dev] = (uint32_t*)ptr;
-    }
-    int slot;
-    if (capturing) {
-        if (captured_next[dev] >= kSchedSlots - kSchedRing) return nullptr;
-        slot = kSchedRing + captured_next[dev]++;
+    std::lock_guard<std::mutex> lock(g_sched_mu);
+    SchedDevice& sd = g_sched[dev];
+    if (!sd.pool) return nullptr;
+    int slot = -1;
+    if (cs != hipStreamCaptureStatusNone) {
+        if (sd.captured_next >= kSchedSlots - kSchedStreamSlots) return nullptr;
+        slot = kSchedStreamSlots + sd.captured_next++;
     } else {
-        slot = ring_next[dev];
-        ring_next[dev] = (slot + 1) % kSchedRing;
+        for (int i = 0; i < sd.n_streams; ++i)
+            if (sd.streams[i] == st) slot = i;
+        if (slot < 0) {
+            if (sd.n_streams >= kSchedStreamSlots) return nullptr;
+            slot = sd.n_streams++;
+            sd.streams[slot] = st;
+        }
     }
-    return pool[dev] + 2 * slot;
+    return sd.pool + 2 * slot;
 }
 
-template <typename T, int D, bool LSE, bool PSTATE, bool BATCH>
+template <typename T, int D, bool LSE, bool PSTATE, bool BATCH, bool DBG = false>
 static int launch_stream_t(const TreeParams& p, const SubtreePlan& plan, hipStream_t st) {
     using Geo = StreamGeom<D>;
     const int64_t n_work = (int64_t)p.B * p.Hkv * plan.total_tiles;
@@ -784,8 +886,8 @@ static int launch_stream_t(const TreeParams& p, const SubtreePlan& plan, hipStre
         set_error("subtree kernel: batch %d exceeds %d sequences", p.B, kCuCache - 1);
         return QATTN_ERR_ARG;
     }
-    const size_t lds = Geo::LDS_BYTES;
-    auto kern = tree_stream_kernel<T, D, LSE, PSTATE, BATCH>;
+    const size_t lds = Geo::LDS_BYTES + (DBG ? Geo::DBG_BYTES : 0);
+    auto kern = tree_stream_kernel<T, D, LSE, PSTATE, BATCH, DBG>;
     int dev = 0, cus = 0, per_cu = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
@@ -822,6 +924,20 @@ static int launch_stream_t(const TreeParams& p, const SubtreePlan& plan, hipStre
 
 int launch_stream(const TreeParams& p, const SubtreePlan& plan, int dtype, int head_dim, bool pstate,
                   hipStream_t st) {
+    if (p.dbg_walk) {
+        // walk export: fp16, packed layout, no LSE (the walk does not depend on them)
+        if (dtype != QATTN_DTYPE_F16 || p.lse || !p.cu) {
+            set_error("the walk export runs fp16 calls over packed cu_seqlens without LSE");
+            return QATTN_ERR_ARG;
+        }
+#define QATTN_STREAM_DBG(D) \
+    return pstate ? launch_stream_t<F16, D, false, true, false, true>(p, plan, st) \
+                  : launch_stream_t<F16, D, false, false, false, true>(p, plan, st);
+        if (head_dim == 32) { QATTN_STREAM_DBG(32) }
+        if (head_dim == 64) { QATTN_STREAM_DBG(64) }
+        QATTN_STREAM_DBG(128)
+#undef QATTN_STREAM_DBG
+    }
 #define QATTN_STREAM_B(T, D, B)                                                                \
     if (p.lse) return pstate ? launch_stream_t<T, D, true, true, B>(p, plan, st)                \
                              : launch_stream_t<T, D, true, false, B>(p, plan, st);              \

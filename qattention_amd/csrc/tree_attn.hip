@@ -47,11 +47,16 @@ void set_error(const char* fmt, ...) {
 
 void clear_error() { g_err[0] = 0; }
 
+// The calling thread's walk-export table (qattn_debug_walk), or null.
+static thread_local int32_t* g_dbg_walk = nullptr;
+
 // ---------------------------------------------------------------------------
 // Gather kernel: 4 lanes per (token, q head), 64 pairs per workgroup with the
 // head index fastest, so a workgroup reads 2 tokens' contiguous head rows.
 // ---------------------------------------------------------------------------
-template <typename T, int D, int WALK, int LAYOUT, bool LSE, bool PSTATE, bool BATCH>
+// DBG: the walk-export instantiation (qattn_debug_walk): every query's walk
+// steps are also written to p.dbg_walk.
+template <typename T, int D, int WALK, int LAYOUT, bool LSE, bool PSTATE, bool BATCH, bool DBG = false>
 __global__ __launch_bounds__(kThreads) void tree_gather_kernel(TreeParams p) {
     constexpr int NCH = D / 32;
     constexpr int SLOTS = kThreads / 4;
@@ -74,8 +79,15 @@ __global__ __launch_bounds__(kThreads) void tree_gather_kernel(TreeParams p) {
     // (a paged step without a valid page reads this query's own Q row)
     const uint16_t* qdummy = (const uint16_t*)p.q + qrow * p.sq_t + (BATCH ? (int64_t)seq * p.sq_b : 0) +
                              (int64_t)h * p.sq_h + 8 * j;
-    Walk4<T, D, WALK, LAYOUT, 8 / (D / 32), BATCH> w(p, seq, start, n, tok, h / p.group, j,
-                                                     LAYOUT == KV_PAGED ? qdummy : nullptr);
+    int32_t* dbg = nullptr;
+    if constexpr (DBG) {
+        if (j == 0) {
+            dbg = p.dbg_walk + (qrow * p.Hq + h) * (p.max_depth + 1);
+            for (int i = 0; i <= p.max_depth; ++i) dbg[i] = -1;
+        }
+    }
+    Walk4<T, D, WALK, LAYOUT, 8 / (D / 32), BATCH, DBG> w(p, seq, start, n, tok, h / p.group, j,
+                                                          LAYOUT == KV_PAGED ? qdummy : nullptr, dbg);
     w.issue();
     if constexpr (PSTATE) {
         load_partial_state4<D>(p, qrow, h, j, m, l, acc);
@@ -287,7 +299,7 @@ static bool make_subtree_plan(int b, int64_t n, int max_depth, int rcap, int nca
     return rows <= rcap;
 }
 
-template <typename T, int D, int WALK, int LAYOUT, bool LSE, bool PSTATE, bool BATCH = false>
+template <typename T, int D, int WALK, int LAYOUT, bool LSE, bool PSTATE, bool BATCH = false, bool DBG = false>
 static int launch_gather(const TreeParams& p, hipStream_t st) {
     constexpr int SLOTS = kThreads / 4;  // 4 lanes per (token, q head)
     const int64_t slots = (int64_t)p.B * p.max_seqlen * p.Hq;
@@ -296,7 +308,7 @@ static int launch_gather(const TreeParams& p, hipStream_t st) {
         set_error("grid too large (%lld blocks)", (long long)blocks);
         return QATTN_ERR_ARG;
     }
-    hipLaunchKernelGGL((tree_gather_kernel<T, D, WALK, LAYOUT, LSE, PSTATE, BATCH>), dim3((unsigned)blocks),
+    hipLaunchKernelGGL((tree_gather_kernel<T, D, WALK, LAYOUT, LSE, PSTATE, BATCH, DBG>), dim3((unsigned)blocks),
                        dim3(kThreads), 0, st, p);
     return launch_status("tree_gather_kernel");
 }
@@ -334,6 +346,19 @@ static int dispatch_tree(const TreeParams& p, int walk, int layout, bool lse, bo
     } else if (algo == QATTN_ALGO_SUBTREE) {
         set_error("the subtree kernel supports the heap walk on packed K/V only");
         return QATTN_ERR_ARG;
+    }
+    if (p.dbg_walk) {
+        // walk export: fp16, packed cu_seqlens, no LSE (the walk does not depend on them)
+        if (T::kCode != QATTN_DTYPE_F16 || lse || !p.cu) {
+            set_error("the walk export runs fp16 calls over packed cu_seqlens without LSE");
+            return QATTN_ERR_ARG;
+        }
+        if (layout == KV_PAGED) return launch_gather<F16, D, WALK_HEAP, KV_PAGED, false, false, false, true>(p, st);
+        if (walk == WALK_HEAP)
+            return pstate ? launch_gather<F16, D, WALK_HEAP, KV_PACKED, false, true, false, true>(p, st)
+                          : launch_gather<F16, D, WALK_HEAP, KV_PACKED, false, false, false, true>(p, st);
+        return pstate ? launch_gather<F16, D, WALK_PARENTS, KV_PACKED, false, true, false, true>(p, st)
+                      : launch_gather<F16, D, WALK_PARENTS, KV_PACKED, false, false, false, true>(p, st);
     }
     if (layout == KV_PACKED) {
         // (a null cu is a uniform batch: its addressing is compiled separately)
@@ -416,6 +441,7 @@ int fill_tree_params(TreeParams& p, const void* q, const int64_t* qs, const void
     p.max_depth = max_depth;
     p.bdiv = make_divider(b);
     p.scale_log2 = scale * kLog2e;
+    p.dbg_walk = g_dbg_walk;
     return QATTN_OK;
 }
 
@@ -428,6 +454,11 @@ extern "C" {
 const char* qattn_version(void) { return "qattention_amd 0.1.0 (gfx950)"; }
 
 const char* qattn_last_error(void) { return g_err; }
+
+int qattn_debug_walk(int32_t* out) {
+    g_dbg_walk = out;
+    return QATTN_OK;
+}
 
 int qattn_tree_fwd(const void* q, const int64_t q_stride[3], const void* k, const int64_t k_stride[3],
                    const void* v, const int64_t v_stride[3], void* o, const int64_t o_stride[3], float* lse,

@@ -14,7 +14,8 @@
 
 namespace qattn {
 
-enum { WALK_HEAP = 0, WALK_PARENTS = 1 };
+// WALK_NONE: no tree keys (the prefix-only pass of the prefix kernel)
+enum { WALK_HEAP = 0, WALK_PARENTS = 1, WALK_NONE = 2 };
 enum { KV_PACKED = 0, KV_PAGED = 1 };
 
 __device__ __forceinline__ int rl(int v, int i) { return __builtin_amdgcn_readlane(v, i); }
@@ -184,7 +185,8 @@ __device__ __forceinline__ void fold_scores(const float* s, const Vec16 (*vf)[NC
 // the walk stops once every lane's walk has stalled (root reached or
 // self-loop).  A caller may issue the first chunk before it builds the
 // initial state, so those loads overlap its own.
-template <typename T, int D, int WALK, int LAYOUT, int CH_ = 8 / (D / 32), bool BATCH = false>
+// DBG (walk export): every step's attended node (or -1) is written to dbg[step].
+template <typename T, int D, int WALK, int LAYOUT, int CH_ = 8 / (D / 32), bool BATCH = false, bool DBG = false>
 struct Walk4 {
     static constexpr int NCH = D / 32;
     static constexpr int CH = CH_;  // default 2 steps at D=128: 64 VGPRs of K/V loads in flight per lane
@@ -200,13 +202,20 @@ struct Walk4 {
     int s0;
     bool val[CH];
     Vec16 kf[CH][NCH], vf[CH][NCH];
+    int32_t* dbg;  // DBG only: this query's row of the walk export (written by lane 0 of the group)
 
     __device__ __forceinline__ Walk4(const TreeParams& p_, int seq_, int32_t start_, int32_t n_, int tok, int kvh,
-                                     int j, const uint16_t* qdummy_ = nullptr)
+                                     int j, const uint16_t* qdummy_ = nullptr, int32_t* dbg_ = nullptr)
         : p(p_), seq(seq_), pb(parents_base<BATCH>(p_, seq_, start_)), n(n_), kvb(kv_base(p_, seq_, start_)),
           kb((const uint16_t*)p_.k + (int64_t)kvh * p_.sk_h + 8 * j),
           vb((const uint16_t*)p_.v + (int64_t)kvh * p_.sv_h + 8 * j), tok0(tok), qdummy(qdummy_), cur(tok),
-          prev(-1), s0(0) {}
+          prev(-1), s0(0), dbg(dbg_) {}
+
+    __device__ __forceinline__ void record(int step, int32_t node) {
+        if constexpr (DBG) {
+            if (dbg && step <= p.max_depth) dbg[step] = node;
+        }
+    }
 
     // Issue the K/V loads of steps s0 .. s0 + CH - 1.  A parents walk asks
     // for each step's next node before that step's K/V rows: loads complete
@@ -230,6 +239,7 @@ struct Walk4 {
             int32_t par = 0;
             if constexpr (WALK == WALK_PARENTS) par = p.parents[pb + cur];  // src/ragged_attn.py:692-694
             val[t] = ok;
+            record(s0 + t, ok ? cur : -1);
             const int32_t row = ok ? cur : tok0;
             const uint16_t* kr = kb + (kvb + row) * p.sk_t;
             const uint16_t* vr = vb + (kvb + row) * p.sv_t;
@@ -255,11 +265,12 @@ struct Walk4 {
     // the row's last entry (or, for an empty table, the Q row) and is
     // discarded.
     __device__ __forceinline__ void issue_paged() {
-        int32_t pg[CH], sl[CH];
+        int32_t pg[CH], sl[CH], nd[CH];
         bool okn[CH];
 #pragma unroll
         for (int t = 0; t < CH; ++t) {
             okn[t] = (s0 + t <= p.max_depth) && (cur != prev);
+            nd[t] = cur;
             const int32_t lp = cur / p.page_size;
             sl[t] = cur - lp * p.page_size;
             okn[t] = okn[t] && lp < p.pt_cols;
@@ -275,6 +286,7 @@ struct Walk4 {
         for (int t = 0; t < CH; ++t) {
             const bool ok = okn[t] && pg[t] >= 0 && pg[t] < p.num_pages;
             val[t] = ok;
+            record(s0 + t, ok ? nd[t] : -1);
             const uint16_t* kr = ok ? kb + (int64_t)pg[t] * p.sk_page + (int64_t)sl[t] * p.sk_t : qdummy;
             const uint16_t* vr = ok ? vb + (int64_t)pg[t] * p.sv_page + (int64_t)sl[t] * p.sv_t : qdummy;
 #pragma unroll

@@ -6,9 +6,9 @@ return values and error behaviour follow the reference; the work is done by
 hand-written gfx950 HIP kernels in libqattn.so, called through its C ABI
 (include/qattn.h) on torch's current HIP stream.  Outputs are allocated here
 through the torch caching allocator.  A call is HIP-graph capturable when
-max_seqlen is given (no host sync); inside the library the only allocation is
-a per-device pool of work-schedule counters, made by the first uncaptured call
-that launches the subtree kernel on a device.
+max_seqlen is given (no host sync).  The library itself allocates nothing;
+the first call on a device runs qattn_init() there (outside graph capture),
+which sets up the subtree kernel's schedule counters.
 
 Differences from the reference, all supersets:
   * K/V may carry fewer heads than Q (GQA): q head h reads kv head
@@ -72,6 +72,7 @@ def _require_device(*ts):
 
 
 def _stream(device) -> int:
+    _lib.ensure_init(device)
     return torch.cuda.current_stream(device).cuda_stream
 
 
@@ -456,6 +457,66 @@ def ragged_attention_prefix(
     O, LSE = _prefix_tree_forward(Q, K, V, cu_dev, B, ms, K_prefix if L else None, kp_stride,
                                   V_prefix if L else None, vp_stride, L, branching_factor, max_depth, 0, 0,
                                   return_lse, num_splits, par)
+    return (O, LSE) if return_lse else O
+
+
+def prefix_attention(
+    Q: torch.Tensor,
+    K_prefix: torch.Tensor,
+    V_prefix: torch.Tensor,
+    cu_seqlens: Optional[torch.Tensor] = None,
+    max_seqlen: int = None,
+    return_lse: bool = True,
+    num_splits: int = 0,
+):
+    """Attention of packed queries over a prefix KV cache only, with LSE: the
+    prefix pass of the reference's verify pipelines, GQA-native.
+
+    Replaces flashinfer.single_prefill_with_kv_cache_return_lse(Q, K_sh, V_sh,
+    causal=False) as scripts/benchmark_micro.py:574-580 calls it (a prefix
+    [L, Hkv, D] shared by every query; cu_seqlens None: all of Q is one
+    sequence) and the aten flash prefix pass with LSE of the E2E verify step
+    (scripts/e2e_benchmark.py:1438-1448; K_prefix [B, L, Hkv, D], one prefix
+    per sequence of cu_seqlens).  Its output merges with a tree pass through
+    fused_lse_merge.  Returns O [T, Hq, D] (and LSE [T, Hq] fp32, natural
+    log, if return_lse)."""
+    if Q.dtype not in _SUPPORTED or K_prefix.dtype != Q.dtype or V_prefix.dtype != Q.dtype:
+        raise AssertionError(f"Inputs must be fp16 or bf16 (got {Q.dtype})")
+    device = _require_device(Q, K_prefix, V_prefix)
+    T, Hq, D = Q.shape
+    shared = K_prefix.dim() == 3
+    if shared:
+        K_prefix, V_prefix = K_prefix.unsqueeze(0), V_prefix.unsqueeze(0)
+    Hkv = K_prefix.shape[2]
+    if cu_seqlens is None:
+        cu_seqlens = torch.tensor([0, T], dtype=torch.int32, device=device)
+        max_seqlen = T
+    B = int(cu_seqlens.shape[0]) - 1
+    if (K_prefix.shape != V_prefix.shape or K_prefix.shape[3] != D or Hkv < 1 or Hq % Hkv
+            or (not shared and K_prefix.shape[0] != B)):
+        raise ValueError(f"prefix shape {tuple(K_prefix.shape)} incompatible with Q {tuple(Q.shape)}, B={B}")
+    L = int(K_prefix.shape[1])
+    if L < 1:
+        raise ValueError("prefix_attention needs a prefix of at least one row")
+    ms, cu_dev = _seqlens(cu_seqlens, B, device, max_seqlen)
+    Q, K_prefix, V_prefix = _vec(Q), _vec(K_prefix), _vec(V_prefix)
+    kp_stride = (0 if shared else K_prefix.stride(0), K_prefix.stride(1), K_prefix.stride(2))
+    vp_stride = (0 if shared else V_prefix.stride(0), V_prefix.stride(1), V_prefix.stride(2))
+    O = torch.empty_like(Q)
+    if not _vec_ok(O):
+        O = torch.empty(Q.shape, dtype=Q.dtype, device=device)
+    LSE = torch.empty(T, Hq, dtype=torch.float32, device=device) if return_lse else None
+    lib = _lib.lib()
+    ws_bytes = int(lib.qattn_prefix_workspace_bytes(B, ms, T, Hq, Hkv, D, L, int(num_splits))) if T else 0
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=device)
+    with torch.cuda.device(device):
+        rc = lib.qattn_prefix_fwd(
+            Q.data_ptr(), _lib.i64arr(Q.stride()), K_prefix.data_ptr(), _lib.i64arr(kp_stride),
+            V_prefix.data_ptr(), _lib.i64arr(vp_stride), L, O.data_ptr(), _lib.i64arr(O.stride()),
+            _lib.ptr(LSE), _lib.i64arr(LSE.stride()) if LSE is not None else None, cu_dev.data_ptr(),
+            B, ms, T, Hq, Hkv, D, 1.0 / math.sqrt(D), _dtype_code(Q), ws.data_ptr(), ws_bytes,
+            int(num_splits), _stream(device))
+    _lib.check(rc, "qattn_prefix_fwd")
     return (O, LSE) if return_lse else O
 
 

@@ -5,6 +5,7 @@ from qattention_amd.ragged_attn import (  # noqa: F401
     build_paged_kv,
     fused_lse_merge,
     pack_inputs,
+    prefix_attention,
     ragged_attention,
     ragged_attention_hybrid,
     ragged_attention_paged,

@@ -79,3 +79,35 @@ def test_more_than_one_gpu_is_refused():
     r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"],
                        capture_output=True, text=True, timeout=120)
     assert r.returncode == 2 and "one GPU" in r.stdout + r.stderr
+
+
+def test_prefix_only_costs():
+    """cfg4's prefix pass alone: Q + O at Hq and the prefix K/V at Hkv; the
+    prefix FLOPs of the verify call."""
+    c = bench.CONFIGS["cfg4_prefix"]
+    alg_bytes, flops, prefix_flops = bench.model_costs(c)
+    T = 4 * 85
+    assert alg_bytes == 2 * T * 128 * 2 * 32 + 2 * 2 * 4 * 10240 * 8 * 128
+    assert flops == prefix_flops == 4 * 4 * 85 * 32 * 10240 * 128
+    assert prefix_flops == bench.model_costs(bench.CONFIGS["cfg4"])[2]
+
+
+@pytest.mark.parametrize("name", sorted(bench.CONFIGS))
+def test_rotation_defeats_the_infinity_cache(name):
+    """Every config rotates enough input sets that a set comes back only after
+    more than 256 MB of other sets (or one set exceeds it), at least 4 sets
+    below 512 MB per set, and the graphs' calls cover the run in order with
+    no call reading the set of the call before it."""
+    alg_bytes = bench.model_costs(bench.CONFIGS[name])[0]
+    n = bench.n_sets(alg_bytes)
+    assert n >= 2
+    if alg_bytes <= 512_000_000:
+        assert n >= 4 and (n * alg_bytes > 512_000_000 or n == 64)
+    assert (n - 1) * alg_bytes > 256_000_000 or n == 64
+    for start, steps in ((0, 20), (5, 20), (3, 1), (0, 8), (16, 200)):
+        chunks = bench.rotation_chunks(start, steps)
+        calls = [s0 + k for s0, m in chunks for k in range(m)]
+        assert calls == list(range(start, start + steps))
+        assert all(m <= bench.CALLS_PER_GRAPH for _, m in chunks)
+        sets = [k % n for k in calls]
+        assert all(a != b for a, b in zip(sets, sets[1:]))

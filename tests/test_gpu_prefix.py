@@ -225,25 +225,31 @@ def test_cfg4_full_size():
     check_fp16(O.double().cpu().numpy(), ref.double().numpy(), "cfg4")
 
 
-def test_cfg5_sampled():
+def test_cfg5_every_sequence():
     """B=16, L=2048, b=8 d=4 (N=4681), H=32, sigma=0.5: the GPU runs the full
-    configuration; the oracle checks sequences 0 and 15 on 4 heads each."""
+    configuration; the padded-SDPA oracle (fp32, MATH) checks every token of
+    every sequence -- each sequence's last partial 128-row tile included --
+    on two heads per sequence (heads 2s and 2s+1, so the 16 sequences cover
+    all 32 heads), and every output is finite."""
     ra = _ra()
     B, b, d, H, D, L = 16, 8, 4, 32, 128, 2048
     N = num_tree_nodes(b, d)
     say("cfg5 full size")
     Q, K, V, cu = make_inputs([N] * B, H, D, B * 10000 + b * 100 + d, sigma=0.5)
     Kp, Vp = _prefix(B, L, H, D, B * 10000 + b * 100 + d + 1, sigma=0.5)
-    O = ra.ragged_attention_prefix(Q.to(DEV), K.to(DEV), V.to(DEV), cu, Kp.to(DEV), Vp.to(DEV), b, d)
-    O = O.cpu()
-    assert torch.isfinite(O.float()).all()
+    O, LSE = ra.ragged_attention_prefix(Q.to(DEV), K.to(DEV), V.to(DEV), cu, Kp.to(DEV), Vp.to(DEV), b, d,
+                                        return_lse=True)
+    O, LSE = O.cpu(), LSE.cpu()
+    assert torch.isfinite(O.float()).all() and torch.isfinite(LSE).all()
     m = otree.tree_attention_mask(b, d)
-    for s in (0, 15):
+    for s in range(B):
         rows = slice(s * N, (s + 1) * N)
-        heads = slice(4 * (s % 8), 4 * (s % 8) + 4)
-        ref = sdpa.padded_sdpa([Q[rows, heads]], [K[rows, heads]], [V[rows, heads]], [m],
-                               [Kp[s, :, heads]], [Vp[s, :, heads]])[0][0]
-        check_fp16(O[rows, heads].double().numpy(), ref.double().numpy(), f"cfg5 seq {s}")
+        heads = slice(2 * s, 2 * s + 2)
+        outs, lses = sdpa.padded_sdpa([Q[rows, heads]], [K[rows, heads]], [V[rows, heads]], [m],
+                                      [Kp[s, :, heads]], [Vp[s, :, heads]], return_lse=True)
+        check_fp16(O[rows, heads].double().numpy(), outs[0].double().numpy(), f"cfg5 seq {s}")
+        assert float((LSE[rows, heads] - lses[0]).abs().max()) <= 1e-4, f"cfg5 LSE seq {s}"
+        say("cfg5 seq", s, "ok")
 
 
 @pytest.mark.parametrize("num_splits", [0, 1])

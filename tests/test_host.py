@@ -134,6 +134,33 @@ def test_abi_prefix_stride_limits():
                                            None, 0, 0, None) == -1
 
 
+def test_abi_prefix_only_validation():
+    """qattn_prefix_fwd: no tree keys, so null k/v are fine; an empty prefix,
+    a non-positive scale or a bad prefix layout is rejected before any launch,
+    and a valid layout with forced splits stops at the missing workspace."""
+    L = _lib.lib()
+    ok3 = _lib.i64arr((256, 64, 1))
+    kp = (512 * 256, 256, 64)
+
+    def call(prefix_len=512, kps=kp, scale=0.125, dtype=0, head_dim=64, splits=2, batch=1):
+        return L.qattn_prefix_fwd(FAKE, ok3, FAKE, _lib.i64arr(kps), FAKE, _lib.i64arr(kp), prefix_len,
+                                  FAKE, ok3, None, None, FAKE, batch, 15, 15, 4, 4, head_dim, scale, dtype,
+                                  None, 0, splits, None)
+
+    assert call(prefix_len=0) == -1
+    assert call(scale=0.0) == -1
+    assert call(scale=-0.1) == -1
+    assert call(dtype=3) == -2
+    assert call(head_dim=48) == -3
+    assert call(kps=(512 * 256, 1 << 25, 64)) == -4
+    assert call(kps=(512 * 256, 252, 64)) == -4
+    assert call() == -5
+    assert call(batch=0) == 0
+    # two splits of (m, l, acc) over 15 tokens x 4 heads, each array 256-byte aligned
+    a256 = lambda x: (x + 255) // 256 * 256
+    assert L.qattn_prefix_workspace_bytes(1, 15, 15, 4, 4, 64, 512, 2) == 2 * a256(2 * 60 * 4) + a256(2 * 60 * 64 * 4)
+
+
 def test_abi_ragged_tree_attn_validation():
     """qattn_ragged_tree_attn_fwd over [B, H, N, D] strides: every layout it
     cannot address is rejected before any launch; a valid layout with L = 512
