@@ -324,6 +324,32 @@ int qattn_ragged_tree_attn_fwd(const void *q, const int64_t q_stride[4],
                                int32_t num_splits, void *stream);
 
 /*
+ * qattn_ragged_tree_attn_fwd without the workspace arguments, for callers
+ * that cannot allocate (code under HIP graph capture that must not touch an
+ * allocator, tight serving loops, harnesses that forbid hipMalloc).  No
+ * counterpart in the reference: it keeps the prefix split states in the
+ * library's static device array `scratch` (32 MiB per device, held until the
+ * process ends) and calls no allocating routine.  The split count is chosen
+ * as by qattn_ragged_tree_attn_fwd; with num_splits 0 it is lowered until
+ * the split states fit the 32 MiB (one split needs none), an explicit
+ * num_splits whose states do not fit returns QATTN_ERR_WORKSPACE.  Every
+ * call on a device shares that device's scratch: calls that overlap in time
+ * on one device (other streams, other threads) race and must not be issued.
+ * Everything else, including the results, is as qattn_ragged_tree_attn_fwd.
+ */
+int qattn_ragged_tree_attn_fwd_noalloc(const void *q, const int64_t q_stride[4],
+                                       const void *k, const int64_t k_stride[4],
+                                       const void *v, const int64_t v_stride[4],
+                                       void *o, const int64_t o_stride[4],
+                                       float *lse, const int64_t lse_stride[3],
+                                       const int32_t *parents, int64_t parents_stride,
+                                       int32_t batch, int32_t num_tree, int32_t num_prefix,
+                                       int32_t num_q_heads, int32_t num_kv_heads,
+                                       int32_t head_dim, int32_t branching_factor,
+                                       int32_t max_depth, float scale, int32_t dtype,
+                                       int32_t num_splits, void *stream);
+
+/*
  * Two-state softmax merge.
  *
  * Replaces _fused_lse_merge_kernel (src/ragged_attn.py:1575-1616) launched by

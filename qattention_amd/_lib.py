@@ -65,6 +65,9 @@ SIGNATURES = {
     "qattn_ragged_tree_attn_fwd": (C.c_int, [
         _p, _i64p, _p, _i64p, _p, _i64p, _p, _i64p, _p, _i64p, _p, _i64,
         _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _i32, _p, _i64, _i32, _p]),
+    "qattn_ragged_tree_attn_fwd_noalloc": (C.c_int, [
+        _p, _i64p, _p, _i64p, _p, _i64p, _p, _i64p, _p, _i64p, _p, _i64,
+        _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _i32, _i32, _p]),
     "qattn_lse_merge": (C.c_int, [
         _p, _i64p, _p, _i64p, _p, _i64p, _p, _i64p, _p, _i64p,
         _i32, _i32, _i32, _i32, _i32, _p]),

@@ -23,6 +23,7 @@
 //    state to the ancestor walk in the same workgroup (gather_walk4), which
 //    normalises and stores O -- no partial state leaves the chip.
 #include <algorithm>
+#include <mutex>
 
 #include "qattn_common.h"
 #include "qattn_device.h"
@@ -968,6 +969,42 @@ static int ragged_tree_attn_impl(const void* q, const int64_t q_stride[4], const
                             parents ? WALK_PARENTS : WALK_HEAP);
 }
 
+// ---------------------------------------------------------------------------
+// Scratch of the allocation-free entry point: a static device array (each GPU
+// the library runs on holds its own copy until the process ends).  Host code
+// never passes `scratch` itself to a kernel (on the host it is only a
+// stand-in for the symbol): it uses the device address from
+// hipGetSymbolAddress, kept per device.
+// ---------------------------------------------------------------------------
+constexpr int64_t kScratchBytes = int64_t(32) << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+namespace {
+constexpr int kScratchMaxDev = 64;
+std::mutex g_scratch_mu;
+void* g_scratch[kScratchMaxDev] = {};
+}  // namespace
+
+// Device address of the current device's scratch (hipGetSymbolAddress once
+// per device, with that device current), or null with the error set.
+static void* scratch_ptr() {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kScratchMaxDev) {
+        set_error("no usable current device (%d) for the scratch array", dev);
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch[dev]) {
+        void* ptr = nullptr;
+        if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) {
+            set_error("hipGetSymbolAddress(scratch) failed on device %d", dev);
+            return nullptr;
+        }
+        g_scratch[dev] = ptr;
+    }
+    return g_scratch[dev];
+}
+
 extern "C" {
 
 int qattn_init(void) {
@@ -977,7 +1014,9 @@ int qattn_init(void) {
         set_error("hipGetDevice failed");
         return QATTN_ERR_HIP;
     }
-    return sched_init(dev);
+    const int rc = sched_init(dev);
+    if (rc) return rc;
+    return scratch_ptr() ? QATTN_OK : QATTN_ERR_HIP;
 }
 
 int64_t qattn_prefix_workspace_bytes(int32_t batch, int32_t max_seqlen, int64_t total_tokens, int32_t num_q_heads,
@@ -1056,6 +1095,41 @@ int qattn_ragged_tree_attn_fwd(const void* q, const int64_t q_stride[4], const v
                                  parents_stride, batch, num_tree, num_prefix, num_q_heads, num_kv_heads, head_dim,
                                  branching_factor, max_depth, scale, dtype, workspace, workspace_size, num_splits,
                                  stream);
+}
+
+int qattn_ragged_tree_attn_fwd_noalloc(const void* q, const int64_t q_stride[4], const void* k,
+                                       const int64_t k_stride[4], const void* v, const int64_t v_stride[4], void* o,
+                                       const int64_t o_stride[4], float* lse, const int64_t lse_stride[3],
+                                       const int32_t* parents, int64_t parents_stride, int32_t batch,
+                                       int32_t num_tree, int32_t num_prefix, int32_t num_q_heads,
+                                       int32_t num_kv_heads, int32_t head_dim, int32_t branching_factor,
+                                       int32_t max_depth, float scale, int32_t dtype, int32_t num_splits,
+                                       void* stream) {
+    clear_error();
+    if (batch > 0 && num_tree > 0 && num_prefix > 0 && num_q_heads > 0 && num_kv_heads > 0 &&
+        num_q_heads % num_kv_heads == 0 && num_splits >= 0) {
+        // the split states must fit the scratch array: the automatic count
+        // drops to the largest that fits (one split needs none), an explicit
+        // one that does not fit is an error
+        const int64_t total = (int64_t)batch * num_tree;
+        const int64_t ups = units_per_split(batch, num_kv_heads, num_tree, num_q_heads / num_kv_heads);
+        int bps = 0;
+        int s = prefix_splits(ups, num_prefix, num_splits, bps);
+        if (workspace_bytes(total, num_q_heads, head_dim, s) > kScratchBytes) {
+            if (num_splits > 0) {
+                set_error("%d prefix splits need %lld bytes of split state; the scratch array holds %lld",
+                          s, (long long)workspace_bytes(total, num_q_heads, head_dim, s), (long long)kScratchBytes);
+                return QATTN_ERR_WORKSPACE;
+            }
+            while (s > 1 && workspace_bytes(total, num_q_heads, head_dim, s) > kScratchBytes) --s;
+            num_splits = s;
+        }
+    }
+    void* ws = scratch_ptr();
+    if (!ws) return QATTN_ERR_HIP;
+    return ragged_tree_attn_impl(q, q_stride, k, k_stride, v, v_stride, o, o_stride, lse, lse_stride, parents,
+                                 parents_stride, batch, num_tree, num_prefix, num_q_heads, num_kv_heads, head_dim,
+                                 branching_factor, max_depth, scale, dtype, ws, kScratchBytes, num_splits, stream);
 }
 
 }  // extern "C"
