@@ -19,7 +19,7 @@ LIB = os.path.join(BUILD_DIR, "libqattn_oracle.so")
 def build(verbose: bool = False) -> str:
     os.makedirs(BUILD_DIR, exist_ok=True)
     tmp = LIB + ".tmp"
-    cmd = ["gcc", "-O2", "-fPIC", "-shared", "-std=c11", "-Wall", "-Wextra",
+    cmd = ["gcc", "-O2", "-fPIC", "-shared", "-std=c11", "-fopenmp", "-Wall", "-Wextra",
            "-o", tmp, SRC, "-lm"]
     if verbose:
         print(" ".join(cmd), flush=True)

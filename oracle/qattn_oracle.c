@@ -111,17 +111,31 @@ void oracle_ancestor_table_parents(const int32_t *cu, int B, const int32_t *pare
  *   q  [T][Hq][D],  k/v  [T][Hkv][D],  anc [T][S1]
  *   kp/vp (optional, L > 0) [B][L][Hkv][D]
  *   o  [T][Hq][D] double,  lse [T][Hq] double (optional)
- * nthreads > 1 is not used here: the loops are plain and sequential. */
+ * Tokens are independent, so an OpenMP build spreads them over threads; each
+ * output is still summed in the same order by one thread (deterministic). */
 void oracle_tree_attn(const float *q, const float *k, const float *v,
                       const int32_t *cu, int B, int Hq, int Hkv, int D,
                       const int32_t *anc, int S1,
                       const float *kp, const float *vp, int L,
                       double scale, double *o, double *lse) {
     const int g = Hq / Hkv;
-    double *scores = (double *)malloc(sizeof(double) * (size_t)(L + S1));
-    int64_t *rows = (int64_t *)malloc(sizeof(int64_t) * (size_t)(L + S1));
-    for (int seq = 0; seq < B; ++seq) {
-        for (int32_t t = cu[seq]; t < cu[seq + 1]; ++t) {
+    if (B <= 0) return;
+    /* tokens [cu[0], cu[B]); rows outside every sequence are left untouched */
+    const int32_t t_lo = cu[0], t_hi = cu[B];
+#pragma omp parallel
+    {
+        double *scores = (double *)malloc(sizeof(double) * (size_t)(L + S1));
+        int64_t *rows = (int64_t *)malloc(sizeof(int64_t) * (size_t)(L + S1));
+#pragma omp for schedule(dynamic, 64)
+        for (int32_t t = t_lo; t < t_hi; ++t) {
+            /* sequence of token t: the last seq with cu[seq] <= t (cu is
+             * non-decreasing, so cu[seq + 1] > t) */
+            int lo = 0, hi = B - 1;
+            while (lo < hi) {
+                int mid = (lo + hi + 1) / 2;
+                if (cu[mid] <= t) lo = mid; else hi = mid - 1;
+            }
+            const int seq = lo;
             for (int h = 0; h < Hq; ++h) {
                 const int kvh = h / g;
                 const float *qr = q + ((int64_t)t * Hq + h) * D;
@@ -174,9 +188,9 @@ void oracle_tree_attn(const float *q, const float *k, const float *v,
                 if (lse) lse[(int64_t)t * Hq + h] = m + log(l_safe);
             }
         }
+        free(scores);
+        free(rows);
     }
-    free(scores);
-    free(rows);
 }
 
 /* Two-state softmax merge, double precision.

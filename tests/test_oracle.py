@@ -184,6 +184,19 @@ def test_ragged_and_truncated_match_padded_sdpa():
         assert np.abs(lse - L.numpy()).max() < 2e-5
 
 
+def test_shifted_cu_equals_rebased_cu():
+    """cu_seqlens that start past row 0 (and leave rows after cu[B]): the
+    tokens in [cu[0], cu[B]) get the attention of the same sequences rebased
+    to row 0, and the rows outside every sequence are never read or written."""
+    lens = [15, 10, 0, 15]
+    Q, K, V, cu = make_inputs([5] + lens + [7], 4, 64, 515, torch.float32)
+    cu = cu[1:-1].clone()  # sequences start at row 5; rows 45..51 belong to none
+    o, lse, _ = oracle_tree(Q, K, V, cu, 2, 3)
+    lo, hi = int(cu[0]), int(cu[-1])
+    o0, lse0, _ = oracle_tree(Q[lo:hi], K[lo:hi], V[lo:hi], cu - cu[0], 2, 3)
+    assert np.array_equal(o[lo:hi], o0) and np.array_equal(lse[lo:hi], lse0)
+
+
 def test_chain_is_causal_attention():
     """b=1 with max_depth >= n-1 is plain causal attention (tests/test_correctness.py:339-350)."""
     n, H, D = 9, 4, 64
