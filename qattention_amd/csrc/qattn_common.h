@@ -107,6 +107,13 @@ struct SubtreePlan {
     int32_t chain_h;                  // b == 1: levels per tile
     int32_t tile_base[kMaxBands];     // first tile of band i; INT32_MAX past the last band
     uint32_t band[kMaxBands];         // lo | hi << 8 | G << 16
+    // Heap level tables for l = 0..63: lvl_start[l] = (b^l - 1) / (b - 1),
+    // the first node of BFS level l (INT32_MAX once it passes that), and
+    // lvl_pow[l] = b^l (UINT32_MAX once it passes that); b == 1: l and 1.
+    // Descendants j levels below node x start at x * b^j + lvl_start[j], and
+    // the ancestor k levels above x is (x - lvl_start[k]) / b^k.
+    int32_t lvl_start[64];
+    uint32_t lvl_pow[64];
 };
 
 // Launch arguments of the persistent subtree kernel (subtree_stream.hip).

@@ -62,7 +62,7 @@ struct StreamGeom {
     static constexpr int NC = D / 32;                 // 32-element k-chunks of Q K^T
     static constexpr int ND = D / 16;                 // 16-row d-tiles of O^T
     static constexpr size_t LDS_BYTES = ((size_t)(KV_ROWS + Q_ROWS + V_ROWS) * PITCH) * 2 +
-                                        (size_t)Q_ROWS * sizeof(QueryEntry) + kCuCache * 4 + 16;
+                                        (size_t)Q_ROWS * sizeof(QueryEntry) + kCuCache * 4 + 16 + 128 * 4;
     // walk export only: the staged row maps (node of each K/V row, token and
     // head offset of each Q row)
     static constexpr size_t DBG_BYTES = (size_t)(KV_ROWS + Q_ROWS) * 4;
@@ -108,17 +108,46 @@ __device__ __forceinline__ int tile_seq(const StreamArgs& sa, int w) {
     return divide(divide(w, sa.tiles_div), sa.hkv_div);
 }
 
+// Inclusive prefix sum over the 64 lanes of a wave: row_shr steps within
+// each 16-lane row (lanes without a source add 0), then the row totals.
+__device__ __forceinline__ int wave_incl_sum(int x) {
+    int v = x;
+    v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, true);  // row_shr:1
+    v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, true);  // row_shr:2
+    v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, true);  // row_shr:4
+    v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, true);  // row_shr:8
+    const int lane = threadIdx.x & 63;
+    const int t0 = __builtin_amdgcn_readlane(v, 15), t1 = __builtin_amdgcn_readlane(v, 31),
+              t2 = __builtin_amdgcn_readlane(v, 47);
+    return v + (lane >= 16 ? t0 : 0) + (lane >= 32 ? t1 : 0) + (lane >= 48 ? t2 : 0);
+}
+
+// Lane i's value of x on every lane that asks for lane idx (0..63).
+__device__ __forceinline__ int lane_get(int x, int idx) { return __builtin_amdgcn_ds_bpermute(idx << 2, x); }
+
 // Which tile w is, and its level table (src/ragged_attn.py:376-377 walk:
 // the ancestors of roots r0..r1-1 at level lo are, per level, one contiguous
 // node range), for a sequence spanning tokens [s, e) (cu_seqlens[seq],
 // cu_seqlens[seq + 1], wave-uniform).  Returns true when the level table was
 // (re)computed, false when it was taken from prev (same tile index and
 // sequence length).  band_tb / band_pk: lane i holds plan.tile_base[i] /
-// plan.band[i] (INT32_MAX / 0 past the bands), loaded once per workgroup.
-template <int D>
+// plan.band[i] (INT32_MAX / 0 past the bands), loaded once per workgroup;
+// lvl_st / lvl_pw: lane l holds plan.lvl_start[l] / plan.lvl_pow[l]; when
+// HAVE_LVL is false they are read here from lvl_lds, the workgroup's LDS copy
+// (a global load in this rarely taken path would make the compiler wait for
+// every load in flight, the next tile's included, before the compute).
+//
+// Every lane works out its own level from the plan's level tables with a few
+// independent operations (the descendants j levels below the root range
+// [r0, r1) span r0 b^j + start(j) .. r1 b^j + start(j) - 1; the ancestors k
+// levels above it are (r0 - start(k)) / b^k .. (r1 - 1 - start(k)) / b^k),
+// and the row and query bases are wave prefix sums: the chain from the first
+// tile's sequence bounds to its first loads stays short.
+template <int D, bool HAVE_LVL>
 __device__ __forceinline__ bool tile_setup_se(const TreeParams& p, const SubtreePlan& plan, const StreamArgs& sa,
                                               int w, int32_t s, int32_t e, const TileMeta& prev, TileMeta& t,
-                                              int32_t band_tb, uint32_t band_pk) {
+                                              int32_t band_tb, uint32_t band_pk, int32_t lvl_st, uint32_t lvl_pw,
+                                              const int32_t* lvl_lds) {
     const int lane = threadIdx.x & 63;
     t.valid = 0;
     t.rows = t.nq = 0;
@@ -151,6 +180,10 @@ __device__ __forceinline__ bool tile_setup_se(const TreeParams& p, const Subtree
         t.kvb = kv_base(p, seq, s);
         return false;
     }
+    if constexpr (!HAVE_LVL) {
+        lvl_st = lvl_lds[lane];
+        lvl_pw = (uint32_t)lvl_lds[64 + lane];
+    }
     const int b = p.bdiv.d;
     // the tile's band: bands cover ascending tile ranges from tile 0
     const int bi = (int)__builtin_popcountll(__ballot(tile >= band_tb)) - 1;
@@ -165,11 +198,8 @@ __device__ __forceinline__ bool tile_setup_se(const TreeParams& p, const Subtree
         r0 = lo;
         r1 = lo + 1;
     } else {
-        int64_t s_lo = 0, w_lo = 1;
-        for (int i = 0; i < lo; ++i) {
-            s_lo += w_lo;
-            w_lo *= b;
-        }
+        const int64_t s_lo = __builtin_amdgcn_readlane(lvl_st, lo);
+        const int64_t w_lo = (uint32_t)__builtin_amdgcn_readlane((int)lvl_pw, lo);
         const int64_t i0 = (int64_t)(tile - tbase) * G;
         r0 = s_lo + i0;
         r1 = s_lo + ((i0 + G < w_lo) ? i0 + G : w_lo);
@@ -179,44 +209,31 @@ __device__ __forceinline__ bool tile_setup_se(const TreeParams& p, const Subtree
 
     const int lam_min = (lo - p.max_depth > 0) ? lo - p.max_depth : 0;
     const int nlev = hi - lam_min + 1;  // <= 64, guaranteed by the host plan
-    int first = 0, cnt = 0;
     const int lam = lam_min + lane;
-    if (lane < nlev) {
-        int64_t f, la;
-        if (lam >= lo) {
-            const int jj = lam - lo;
-            int64_t bj = 1, sj = 0;
-            for (int i = 0; i < jj; ++i) {
-                sj += bj;
-                bj *= b;
-            }
-            f = r0 * bj + sj;
-            la = r1 * bj + sj - 1;
-        } else {
-            int32_t a = (int32_t)r0, c = (int32_t)(r1 - 1);
-            for (int i = 0; i < lo - lam; ++i) {
-                a = heap_parent(a, p.bdiv);
-                c = heap_parent(c, p.bdiv);
-            }
-            f = a;
-            la = c;
-        }
-        if (la > n - 1) la = n - 1;
-        if (f <= la) {
-            first = (int)f;
-            cnt = (int)(la - f + 1);
-        }
+    // level offset from the root level: j >= 0 below, -j above
+    const int j = lam - lo;
+    const int aj = j >= 0 ? j : -j;
+    const int32_t st_j = lane_get(lvl_st, aj < 63 ? aj : 63);
+    const uint32_t pw_j = (uint32_t)lane_get((int)lvl_pw, aj < 63 ? aj : 63);
+    int64_t f, la;
+    if (j >= 0) {
+        f = (int64_t)((uint64_t)r0 * pw_j) + st_j;
+        la = (int64_t)((uint64_t)r1 * pw_j) + st_j - 1;
+    } else {
+        f = (uint32_t)(r0 - st_j) / pw_j;
+        la = (uint32_t)(r1 - 1 - st_j) / pw_j;
+    }
+    if (la > n - 1) la = n - 1;
+    int first = 0, cnt = 0;
+    if (lane < nlev && f <= la) {
+        first = (int)f;
+        cnt = (int)(la - f + 1);
     }
     // exclusive prefix sums over levels: K/V LDS row base, Q LDS row base
-    const int qc = (lane < nlev && lam >= lo) ? cnt * p.group : 0;
-    int base = 0, qb = 0;
-    for (int i = 0; i < nlev; ++i) {
-        const int c = rl(cnt, i), cq = rl(qc, i);
-        base += (i < lane) ? c : 0;
-        qb += (i < lane) ? cq : 0;
-    }
-    const int rows = rl(base + cnt, nlev - 1);
-    const int nq = rl(qb + qc, nlev - 1);
+    const int qc = (lane < nlev && j >= 0) ? cnt * p.group : 0;
+    const int cend = wave_incl_sum(cnt), qend = wave_incl_sum(qc);
+    const int rows = __builtin_amdgcn_readlane(cend, nlev - 1);
+    const int nq = __builtin_amdgcn_readlane(qend, nlev - 1);
     if (rows > StreamGeom<D>::KV_ROWS || nq > StreamGeom<D>::Q_ROWS) return true;  // not for a host-built plan
     t.start = s;
     t.n = n;
@@ -229,8 +246,8 @@ __device__ __forceinline__ bool tile_setup_se(const TreeParams& p, const Subtree
     t.kvb = kv_base(p, seq, s);
     t.first = first;
     t.cnt = cnt;
-    t.off = base - first;
-    t.qb = qb;
+    t.off = cend - cnt - first;
+    t.qb = qend - qc;
     t.valid = 1;
     return true;
 }
@@ -243,55 +260,50 @@ __device__ __forceinline__ bool tile_setup_se(const TreeParams& p, const Subtree
 template <int D>
 __device__ __forceinline__ bool tile_setup(const TreeParams& p, const SubtreePlan& plan, const StreamArgs& sa,
                                            const int32_t __attribute__((address_space(3)))* cu_lds, int w,
-                                           const TileMeta& prev, TileMeta& t, int32_t band_tb, uint32_t band_pk) {
+                                           const TileMeta& prev, TileMeta& t, int32_t band_tb, uint32_t band_pk,
+                                           const int32_t* lvl_lds) {
     int seq = tile_seq(sa, w);
     seq = seq < p.B ? seq : p.B;  // tile_setup_se rejects seq >= B
     const int32_t s = __builtin_amdgcn_readfirstlane(cu_lds[seq]);
     const int32_t e = __builtin_amdgcn_readfirstlane(cu_lds[seq < p.B ? seq + 1 : seq]);
-    return tile_setup_se<D>(p, plan, sa, w, s, e, prev, t, band_tb, band_pk);
+    return tile_setup_se<D, false>(p, plan, sa, w, s, e, prev, t, band_tb, band_pk, 0, 0u, lvl_lds);
 }
 
+// The load rows of a tile (RowMap) from its level table.  Lane x of each
+// wave works out K/V row x and Q row x of the tile (one pass over the levels
+// with wave-uniform values: row x lies in the last level whose base is <= x),
+// then every thread takes the rows it stages from those lanes.
 template <int D>
 __device__ __forceinline__ void tile_rowmap(const TreeParams& p, const Divider& gdiv, const TileMeta& t,
                                             RowMap<D>& rm) {
     using Geo = StreamGeom<D>;
-    const int tid = threadIdx.x;
-    const int rsub = tid / Geo::CPR, c = tid % Geo::CPR;
-    int kof[Geo::PASSES], qbl[Geo::PASSES], fl[Geo::PASSES];
-    const int o0 = rl(t.off, 0);
-#pragma unroll
-    for (int ps = 0; ps < Geo::PASSES; ++ps) {
-        kof[ps] = o0;
-        qbl[ps] = 0;
-        fl[ps] = 0;
-    }
+    static_assert(Geo::KV_ROWS <= 64 && Geo::Q_ROWS <= 64, "one row per lane");
+    // (nlev <= 64, so z is 0: it keeps the lane and row terms below inside
+    // this rarely taken path instead of live across the whole tile loop)
+    const int z = t.nlev >> 7;
+    const int x = (threadIdx.x + z) & 63;
+    int koff = rl(t.off, 0), qbl = 0, fl = 0;
     for (int i = 0; i < t.nlev; ++i) {
-        const int ci = rl(t.cnt, i);
-        if (ci == 0) continue;
         const int oi = rl(t.off, i), fi = rl(t.first, i);
-        const int bi = oi + fi, qi = rl(t.qb, i);
-#pragma unroll
-        for (int ps = 0; ps < Geo::PASSES; ++ps) {
-            if (ps * Geo::RPP + rsub >= bi) kof[ps] = oi;
-        }
+        if (x >= oi + fi) koff = oi;  // K/V row base of level i
         if (t.lam_min + i >= t.lo) {
-#pragma unroll
-            for (int ps = 0; ps < Geo::PASSES; ++ps) {
-                if (ps * Geo::RPP + rsub >= qi) {
-                    qbl[ps] = qi;
-                    fl[ps] = fi;
-                }
+            const int qi = rl(t.qb, i);
+            if (x >= qi) {
+                qbl = qi;
+                fl = fi;
             }
         }
     }
-    const int g = p.group;
-    (void)c;
+    const int sq = x - qbl;
+    const int nd = divide(sq, gdiv);
+    const int kvnode = x - koff;                                  // K/V row x: node, relative to the tile's kv base
+    const int qpack = ((fl + nd) << 8) | (sq - nd * p.group);     // Q row x: node << 8 | q head in the group
+    const int rsub = (threadIdx.x + z) / Geo::CPR;
 #pragma unroll
     for (int ps = 0; ps < Geo::PASSES; ++ps) {
-        rm.kvrow[ps] = ps * Geo::RPP + rsub - kof[ps];  // K/V row relative to the tile's kv base
-        const int sq = ps * Geo::RPP + rsub - qbl[ps];
-        const int nd = divide(sq, gdiv);
-        rm.qrow[ps] = ((fl[ps] + nd) << 8) | (sq - nd * g);  // group <= Q_ROWS (a plan exists)
+        const int r = ps * Geo::RPP + rsub;  // < 64
+        rm.kvrow[ps] = lane_get(kvnode, r);
+        rm.qrow[ps] = lane_get(qpack, r);  // group <= Q_ROWS (a plan exists)
     }
 }
 
@@ -678,7 +690,8 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void tree_stream_kernel(
     QueryEntry* qtab = reinterpret_cast<QueryEntry*>(Vs + Geo::V_ROWS * Geo::PITCH);
     int32_t* cuc = reinterpret_cast<int32_t*>(qtab + Geo::Q_ROWS);
     int32_t* next_slot = cuc + kCuCache;  // the workgroup's next item, written by thread 0
-    int32_t* dbg_row = next_slot + 4;     // (DBG only: LDS_BYTES + DBG_BYTES are allocated)
+    int32_t* lvl_lds = next_slot + 4;     // plan.lvl_start[0..63], plan.lvl_pow[0..63]
+    int32_t* dbg_row = lvl_lds + 128;     // (DBG only: LDS_BYTES + DBG_BYTES are allocated)
     int32_t* dbg_q = dbg_row + Geo::KV_ROWS;
     const Divider gdiv = sa.gdiv;
 
@@ -702,6 +715,9 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void tree_stream_kernel(
     const int lane = threadIdx.x & 63;
     const int32_t band_tb = lane < kMaxBands ? plan.tile_base[lane] : INT32_MAX;
     const uint32_t band_pk = lane < kMaxBands ? plan.band[lane] : 0u;
+    // the level tables of the first tile's setup, loaded with the band table
+    const int32_t lvl_st0 = plan.lvl_start[lane];
+    const uint32_t lvl_pw0 = plan.lvl_pow[lane];
     // V rows the PV product reads but no tile has written yet must hold finite
     // values (P = 0 multiplies them): zero them once.  Each thread zeroes the
     // V chunks it stages itself, so its own tile stores follow the zeros in
@@ -730,7 +746,12 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void tree_stream_kernel(
                                            : p.cu[threadIdx.x];  // p.B < kCuCache = kStThreads
     const int32_t s0 = BATCH ? seq0 * p.max_seqlen : __builtin_amdgcn_readfirstlane(p.cu[seq0]);
     const int32_t e0 = BATCH ? s0 + p.max_seqlen : __builtin_amdgcn_readfirstlane(p.cu[seq0 + 1]);
-    tile_setup_se<D>(p, plan, sa, w, s0, e0, none, cur, band_tb, band_pk);
+    tile_setup_se<D, true>(p, plan, sa, w, s0, e0, none, cur, band_tb, band_pk, lvl_st0, lvl_pw0, lvl_lds);
+    // the level tables for later tiles' setups (published by the first loop top's barrier)
+    if (threadIdx.x < 64) {
+        lvl_lds[threadIdx.x] = lvl_st0;
+        lvl_lds[64 + threadIdx.x] = (int32_t)lvl_pw0;
+    }
     if (cur.valid) {
         tile_rowmap<D>(p, gdiv, cur, rm);
         tile_issue<D, BATCH>(p, cur, rm, sg);
@@ -759,7 +780,7 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void tree_stream_kernel(
         const int wn = kn * sa.ngroups.d + g;
         TileMeta nxt;
         if (more) {
-            const bool fresh = tile_setup<D>(p, plan, sa, cu_lds, wn, cur, nxt, band_tb, band_pk);
+            const bool fresh = tile_setup<D>(p, plan, sa, cu_lds, wn, cur, nxt, band_tb, band_pk, lvl_lds);
             if (nxt.valid) {
                 if (fresh) tile_rowmap<D>(p, gdiv, nxt, rm);
                 tile_issue<D, BATCH>(p, nxt, rm, sg);

@@ -213,6 +213,15 @@ static bool make_subtree_plan(int b, int64_t n, int max_depth, int rcap, int nca
     plan = SubtreePlan{};
     for (int i = 0; i < kMaxBands; ++i) plan.tile_base[i] = INT32_MAX;
     if (n <= 0 || b < 1) return false;
+    {
+        int64_t st = 0, pw = 1;
+        for (int l = 0; l < 64; ++l) {
+            plan.lvl_start[l] = (int32_t)std::min<int64_t>(st, INT32_MAX);
+            plan.lvl_pow[l] = (uint32_t)std::min<int64_t>(pw, UINT32_MAX);
+            if (st < INT32_MAX) st += pw;
+            if (pw < UINT32_MAX && b > 1) pw = std::min<int64_t>(pw * b, UINT32_MAX);
+        }
+    }
     if (b == 1) {
         const int extra = (int)std::min<int64_t>(max_depth, n - 1);
         int h = std::min(rcap - extra, ncap);
