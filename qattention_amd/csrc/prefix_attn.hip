@@ -68,6 +68,21 @@ __device__ __forceinline__ int kv_swz(int r, int dv) {
 // s_waitcnt immediate (gfx9 encoding): vmcnt N, expcnt and lgkmcnt unconstrained
 constexpr int kWaitVm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 
+// One 1 KB global -> LDS load: global_load_lds_dwordx4 with a wave-uniform
+// base in SGPRs and a 32-bit per-lane byte offset (lane i writes bytes
+// [16 i, 16 i + 16) of the LDS run at dst), so issuing it costs no vector ALU
+// work.  Written as an asm statement, which also keeps the compiler's wait
+// analysis precise: it treats a pending LDS-DMA load as an out-of-order LDS
+// event and would otherwise wait for every LDS read in flight
+// (lgkmcnt(0)) before each use of one.  The kernel orders these loads itself
+// (s_waitcnt vmcnt + barrier before a buffer is read, barrier before it is
+// overwritten).
+__device__ __forceinline__ void lds_dma16(uint32_t voff, const char* sbase, void* dst) {
+    const uint32_t lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)dst;
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds)
+                 : "memory", "m0");
+}
+
 // WALK: the tree walk of the fused epilogue (heap or explicit parents, or
 // none for the prefix-only pass); the split kernels leave the walk to the tree
 // kernels.  DBG: the walk-export instantiation (qattn_debug_walk), which also
@@ -184,12 +199,9 @@ __global__ __launch_bounds__(kPrefixThreads) __attribute__((amdgpu_waves_per_eu(
     auto issue = [&](const char* base, int64_t st, const uint32_t (&off)[NI], int j, uint16_t* buf) {
         const int kb = k_lo + j * kBN;
         const char* gb = base + (int64_t)kb * st;
-        if (kb + kBN <= k_hi) {
+        if (__builtin_expect(kb + kBN <= k_hi, 1)) {
 #pragma unroll
-            for (int i = 0; i < NI; ++i)
-                __builtin_amdgcn_global_load_lds(
-                    (const void*)(gb + off[i]), (__attribute__((address_space(3))) void*)(buf + (wave * NI + i) * 512),
-                    16, 0, 0);
+            for (int i = 0; i < NI; ++i) lds_dma16(off[i], gb, buf + (wave * NI + i) * 512);
         } else {
             // tail block of the split: rows past k_hi - 1 load that key instead
             const int last = k_hi - 1 - kb;
@@ -197,9 +209,7 @@ __global__ __launch_bounds__(kPrefixThreads) __attribute__((amdgpu_waves_per_eu(
             for (int i = 0; i < NI; ++i) {
                 const int row = (wave * NI + i) * RPI + lane / DV;
                 const uint32_t col = 16 * ((lane % DV) ^ kv_swz(row, DV));
-                __builtin_amdgcn_global_load_lds(
-                    (const void*)(gb + (uint32_t)min(row, last) * (uint32_t)st + col),
-                    (__attribute__((address_space(3))) void*)(buf + (wave * NI + i) * 512), 16, 0, 0);
+                lds_dma16((uint32_t)min(row, last) * (uint32_t)st + col, gb, buf + (wave * NI + i) * 512);
             }
         }
     };
