@@ -383,7 +383,7 @@ def build_workload(name, algo, forced_sets=0):
         if layout == "bhnd":
             return ra.ragged_tree_attn(Q, K, V, b, d, parents[:N] if parents_walk else None)
         if layout == "paged":
-            return ra.ragged_attention_paged(Q, K, V, Kp, cu, b, d, max_seqlen=N)
+            return ra._paged_forward(Q, K, V, Kp, cu, b, d, N, False, algo)[0]
         if layout == "merge":
             return ra.fused_lse_merge(Kp, Vp, Q, K)
         if layout == "prefix_only":

@@ -139,7 +139,10 @@ int qattn_tree_parents_fwd(const void *q, const int64_t q_stride[3],
  * {page, slot, head, dim}; page_table is a DEVICE int32 [batch, pt_cols]
  * array (row stride pt_cols).  Ancestor position c of sequence s lives at
  * page page_table[s, c / page_size], slot c % page_size.  A page index outside
- * [0, num_pages) or a logical page beyond pt_cols skips that ancestor.
+ * [0, num_pages) or a logical page beyond pt_cols skips that ancestor; a query
+ * that attends nothing gets o = 0 and lse = -inf.  algo selects the kernel as
+ * for qattn_tree_fwd: the subtree kernel stages each tile's rows once through
+ * LDS and takes batch * pt_cols <= 2048 page-table entries.
  */
 int qattn_tree_paged_fwd(const void *q, const int64_t q_stride[3],
                          const void *k_cache, const int64_t k_stride[4],
@@ -151,7 +154,7 @@ int qattn_tree_paged_fwd(const void *q, const int64_t q_stride[3],
                          int32_t batch, int32_t max_seqlen, int64_t total_tokens,
                          int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
                          int32_t branching_factor, int32_t max_depth, float scale,
-                         int32_t dtype, void *stream);
+                         int32_t dtype, int32_t algo, void *stream);
 
 /*
  * Ancestor index table of the heap walk (parents == NULL) or the

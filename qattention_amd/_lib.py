@@ -48,7 +48,7 @@ SIGNATURES = {
         _p, _p, _i32, _i32, _i64, _i32, _i32, _i32, _i32, _f32, _i32, _p]),
     "qattn_tree_paged_fwd": (C.c_int, [
         _p, _i64p, _p, _i64p, _p, _i64p, _p, _i64p, _p, _i64p,
-        _p, _p, _i32, _i32, _i32, _i32, _i32, _i64, _i32, _i32, _i32, _i32, _i32, _f32, _i32, _p]),
+        _p, _p, _i32, _i32, _i32, _i32, _i32, _i64, _i32, _i32, _i32, _i32, _i32, _f32, _i32, _i32, _p]),
     "qattn_ancestors": (C.c_int, [_p, _p, _i32, _i32, _i64, _i32, _i32, _p, _p]),
     "qattn_prefix_workspace_bytes": (C.c_int64, [_i32, _i32, _i64, _i32, _i32, _i32, _i32, _i32]),
     "qattn_prefix_tree_fwd": (C.c_int, [

@@ -68,6 +68,7 @@ struct TreeParams {
     int32_t num_pages, pt_cols, page_size;
     int32_t B, Hq, Hkv, group, max_seqlen, max_depth;
     Divider bdiv;               // branching factor
+    Divider pdiv;               // paged K/V: page_size
     float scale_log2;           // softmax scale * log2(e)
     // split-K prefix partial state merged into the tree state (may be null)
     const float* part_m;        // [n_split][T][Hq]   running max (log2 domain)
@@ -144,10 +145,13 @@ struct StreamArgs {
 };
 
 // Subtree kernel: rows one tile may stage (K/V rows, Q rows) for head_dim,
-// and the largest batch it takes (its LDS copy of cu_seqlens).
+// the largest batch it takes (its LDS copy of cu_seqlens) and, for paged K/V,
+// the largest page table (B * pt_cols entries, copied to LDS).
 void stream_tile_caps(int head_dim, int* kv_rows, int* q_rows);
 int stream_max_batch();
-int launch_stream(const TreeParams& p, const SubtreePlan& plan, int dtype, int head_dim, bool pstate,
+int stream_max_page_entries();
+// paged: K/V through p.page_table (heap walk, no prefix state)
+int launch_stream(const TreeParams& p, const SubtreePlan& plan, int dtype, int head_dim, bool pstate, bool paged,
                   hipStream_t st);
 // qattn_init's part for the subtree kernel: the device address of the
 // current device's counter pool, zeroed (synchronously, on a private stream).

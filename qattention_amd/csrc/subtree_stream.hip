@@ -38,6 +38,7 @@ namespace qattn {
 
 constexpr int kStThreads = 256;
 constexpr int kCuCache = 256;  // cu_seqlens entries cached in LDS
+constexpr int kPtCache = 2048; // paged K/V: page-table entries cached in LDS (B * pt_cols)
 // s_waitcnt immediate (gfx9 encoding): vmcnt 0, expcnt and lgkmcnt unconstrained
 constexpr int kWaitVmcnt0 = (7 << 4) | (15 << 8);
 
@@ -66,6 +67,9 @@ struct StreamGeom {
     // walk export only: the staged row maps (node of each K/V row, token and
     // head offset of each Q row)
     static constexpr size_t DBG_BYTES = (size_t)(KV_ROWS + Q_ROWS) * 4;
+    // paged K/V only: one flag per K/V row (its page exists) for two tiles,
+    // then the page table (B * pt_cols entries)
+    static constexpr size_t ROWOK_BYTES = (size_t)2 * KV_ROWS * 4;
 };
 
 // Per-tile state.  Scalars are wave-uniform; first/cnt/off/qb are per lane,
@@ -95,6 +99,7 @@ struct Stage {
 };
 
 int stream_max_batch() { return kCuCache - 1; }
+int stream_max_page_entries() { return kPtCache; }
 
 void stream_tile_caps(int head_dim, int* kv_rows, int* q_rows) {
     const int rows = head_dim == 128 ? StreamGeom<128>::KV_ROWS
@@ -308,23 +313,59 @@ __device__ __forceinline__ void tile_rowmap(const TreeParams& p, const Divider& 
 }
 
 // Issue the global loads of a tile into the staging registers.
-template <int D, bool BATCH>
+// PAGED: node x of the sequence lives in slot x % page_size of page
+// pt[seq][x / page_size] (src/ragged_attn.py:822-929); pt_lds is the
+// workgroup's LDS copy of the page table.  A row whose logical page is past
+// pt_cols or whose page is outside [0, num_pages) gets flag 0 in rowok (this
+// tile's half of the double buffer; the compute masks the row out) and reads
+// the tile's first Q row instead (in bounds, and finite whenever an output
+// can be: P = 0 multiplies its V, the mask replaces its score).  Loads stay
+// unconditional (a guarded load made the compiler keep a staged register in
+// scratch and wait for it at issue), and the flags go to LDS at once, so
+// nothing extra stays in registers across the compute of the previous tile.
+template <int D, bool BATCH, bool PAGED>
 __device__ __forceinline__ void tile_issue(const TreeParams& p, const TileMeta& t, const RowMap<D>& rm,
-                                           Stage<D>& sg) {
+                                           Stage<D>& sg, const int32_t* pt_lds, int32_t* rowok) {
     using Geo = StreamGeom<D>;
     const int rsub = threadIdx.x / Geo::CPR;
-    const int c8 = 8 * (threadIdx.x % Geo::CPR);
-    const uint16_t* kg = (const uint16_t*)p.k + (t.kvb * p.sk_t + (int64_t)t.kvh * p.sk_h + c8);
-    const uint16_t* vg = (const uint16_t*)p.v + (t.kvb * p.sv_t + (int64_t)t.kvh * p.sv_h + c8);
+    // (paged: z = 0 from the tile, so the per-lane base pointers below are
+    // formed here rather than kept in registers across the loop)
+    const int z = PAGED ? (t.nlev >> 7) : 0;
+    const int c8 = 8 * ((threadIdx.x + z) % Geo::CPR);
+    const int64_t kvb = PAGED ? 0 : t.kvb;
+    const uint16_t* kg = (const uint16_t*)p.k + (kvb * p.sk_t + (int64_t)t.kvh * p.sk_h + c8);
+    const uint16_t* vg = (const uint16_t*)p.v + (kvb * p.sv_t + (int64_t)t.kvh * p.sv_h + c8);
     const uint16_t* qg =
         (const uint16_t*)p.q +
         ((int64_t)t.start * p.sq_t + (BATCH ? (int64_t)t.seq * p.sq_b : 0) + (int64_t)t.kvh * p.group * p.sq_h + c8);
+    if constexpr (PAGED) {
+        const int32_t* ptrow = pt_lds + t.seq * p.pt_cols;
+        const bool c0 = (threadIdx.x % Geo::CPR) == 0;
 #pragma unroll
-    for (int ps = 0; ps < Geo::PASSES; ++ps) {
-        if (ps * Geo::RPP >= t.rows) break;  // wave-uniform
-        if (ps * Geo::RPP + rsub < t.rows) {
-            sg.k[ps] = ld16(kg + (int64_t)rm.kvrow[ps] * p.sk_t);
-            sg.v[ps] = ld16(vg + (int64_t)rm.kvrow[ps] * p.sv_t);
+        for (int ps = 0; ps < Geo::PASSES; ++ps) {
+            if (ps * Geo::RPP >= t.rows) break;  // wave-uniform
+            const int r = ps * Geo::RPP + rsub;
+            if (r < t.rows) {
+                const int32_t node = rm.kvrow[ps];
+                const int32_t lp = divide(node, p.pdiv);
+                const int32_t slot = node - lp * p.page_size;
+                const int32_t pg = lp < p.pt_cols ? ptrow[lp] : -1;
+                const bool ok = (uint32_t)pg < (uint32_t)p.num_pages;
+                if (c0) rowok[r] = ok ? 1 : 0;
+                const uint16_t* kr = ok ? kg + (int64_t)pg * p.sk_page + (int64_t)slot * p.sk_t : qg;
+                const uint16_t* vr = ok ? vg + (int64_t)pg * p.sv_page + (int64_t)slot * p.sv_t : qg;
+                sg.k[ps] = ld16(kr);
+                sg.v[ps] = ld16(vr);
+            }
+        }
+    } else {
+#pragma unroll
+        for (int ps = 0; ps < Geo::PASSES; ++ps) {
+            if (ps * Geo::RPP >= t.rows) break;  // wave-uniform
+            if (ps * Geo::RPP + rsub < t.rows) {
+                sg.k[ps] = ld16(kg + (int64_t)rm.kvrow[ps] * p.sk_t);
+                sg.v[ps] = ld16(vg + (int64_t)rm.kvrow[ps] * p.sv_t);
+            }
         }
     }
 #pragma unroll
@@ -429,9 +470,9 @@ __device__ __forceinline__ void build_query_table(const TreeParams& p, const Div
 // written as [token][q head][step] (step = the query's depth minus the
 // row's).  A bit on a row without a node, two rows at one step, or a Q row
 // staged from another token/head than the table says marks the entry -2 at
-// step 0.
+// step 0.  vmask: the rows the compute keeps (paged K/V: rows with a page).
 __device__ __forceinline__ void dbg_walk_export(const TreeParams& p, const TileMeta& t, const QueryEntry* qt,
-                                                const int32_t* dbg_row, const int32_t* dbg_q) {
+                                                const int32_t* dbg_row, const int32_t* dbg_q, uint64_t vmask) {
     const int S1 = p.max_depth + 1;
     auto depth = [&](int32_t x) {
         int dd = 0;
@@ -443,7 +484,7 @@ __device__ __forceinline__ void dbg_walk_export(const TreeParams& p, const TileM
     };
     for (int q = threadIdx.x; q < t.nq; q += kStThreads) {
         const QueryEntry qe = qt[q];
-        const uint64_t mask = ((uint64_t)qe.mask_hi << 32) | qe.mask_lo;
+        const uint64_t mask = (((uint64_t)qe.mask_hi << 32) | qe.mask_lo) & vmask;
         bool bad = dbg_q[q] != ((qe.node << 8) | qe.hoff);
         int32_t* out = p.dbg_walk + (((int64_t)t.start + qe.node) * p.Hq + t.kvh * p.group + qe.hoff) * S1;
         for (int i = 0; i < S1; ++i) out[i] = -1;
@@ -465,9 +506,11 @@ __device__ __forceinline__ void dbg_walk_export(const TreeParams& p, const TileM
 }
 
 // One wave: attention of 16 queries (query block qb) of the tile held in LDS.
+// vmask: the K/V rows that exist (all of them but paged rows without a page).
 template <typename T, int D, bool LSE, bool PSTATE, bool BATCH>
 __device__ __forceinline__ void block_compute(const TreeParams& p, const TileMeta& t, int qb, const uint16_t* Ks,
-                                              const uint16_t* Vs, const uint16_t* Qs, const QueryEntry* qt) {
+                                              const uint16_t* Vs, const uint16_t* Qs, const QueryEntry* qt,
+                                              uint64_t vmask) {
     using Geo = StreamGeom<D>;
     constexpr int NC = Geo::NC, ND = Geo::ND, KT = Geo::KT;
     const int lane = threadIdx.x & 63;
@@ -479,7 +522,7 @@ __device__ __forceinline__ void block_compute(const TreeParams& p, const TileMet
     const bool qvalid = sq < t.nq;
     QueryEntry qe = QueryEntry{0u, 0u, 0, 0};
     if (qvalid) qe = qt[sq];
-    const uint64_t mask = ((uint64_t)qe.mask_hi << 32) | qe.mask_lo;
+    const uint64_t mask = (((uint64_t)qe.mask_hi << 32) | qe.mask_lo) & vmask;
     const int64_t qrow = (int64_t)t.start + qe.node;
     const int qh = t.kvh * g + qe.hoff;
 
@@ -630,9 +673,11 @@ __device__ __forceinline__ void block_compute(const TreeParams& p, const TileMet
     const float l_safe = (l == 0.f) ? 1.f : l;  // src/ragged_attn.py:379-380
     const float inv = __builtin_amdgcn_rcpf(l_safe);
     if constexpr (LSE) {
+        // a query that attends nothing (paged rows without a page) has
+        // m = -inf in the reference's formula
         if (qvalid && i4 == 0)
             p.lse[qrow * p.slse_t + (BATCH ? (int64_t)t.seq * p.slse_b : 0) + (int64_t)qh * p.slse_h] =
-                (m + fast_log2(l_safe)) * kLn2;
+                l == 0.f ? -INFINITY : (m + fast_log2(l_safe)) * kLn2;
     }
 
     // ---- O: lane holds O^T[16 dt + 4 i4 + r][c16], stored straight as 8-byte
@@ -652,10 +697,11 @@ __device__ __forceinline__ void block_compute(const TreeParams& p, const TileMet
 
 template <typename T, int D, bool LSE, bool PSTATE, bool BATCH>
 __device__ __forceinline__ void tile_compute(const TreeParams& p, const TileMeta& t, const uint16_t* Ks,
-                                             const uint16_t* Vs, const uint16_t* Qs, const QueryEntry* qt) {
+                                             const uint16_t* Vs, const uint16_t* Qs, const QueryEntry* qt,
+                                             uint64_t vmask) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     for (int qb = wave; 16 * qb < t.nq; qb += kStThreads / 64)
-        block_compute<T, D, LSE, PSTATE, BATCH>(p, t, qb, Ks, Vs, Qs, qt);
+        block_compute<T, D, LSE, PSTATE, BATCH>(p, t, qb, Ks, Vs, Qs, qt, vmask);
 }
 
 // Next item of a group: one returning atomic on the group's counter.
@@ -678,7 +724,9 @@ __device__ __forceinline__ uint32_t sched_grab(uint32_t* ctr) {
 // layout compiles without that addressing.
 // DBG: the walk-export instantiation (qattn_debug_walk), which also writes
 // every query's attended ancestor set to p.dbg_walk.
-template <typename T, int D, bool LSE, bool PSTATE, bool BATCH, bool DBG = false>
+// PAGED: K/V rows from the paged cache through p.page_table (copied to LDS at
+// kernel start; the host launches this only for B * pt_cols <= kPtCache).
+template <typename T, int D, bool LSE, bool PSTATE, bool BATCH, bool DBG = false, bool PAGED = false>
 __global__ __launch_bounds__(kStThreads)
 __attribute__((amdgpu_waves_per_eu(3, 3))) void tree_stream_kernel(
     TreeParams p, SubtreePlan plan, StreamArgs sa) {
@@ -693,7 +741,19 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void tree_stream_kernel(
     int32_t* lvl_lds = next_slot + 4;     // plan.lvl_start[0..63], plan.lvl_pow[0..63]
     int32_t* dbg_row = lvl_lds + 128;     // (DBG only: LDS_BYTES + DBG_BYTES are allocated)
     int32_t* dbg_q = dbg_row + Geo::KV_ROWS;
+    // (PAGED only: ROWOK_BYTES + 4 B * B * pt_cols more are allocated; tile
+    // flags alternate between the two halves of rowok, par selects the half
+    // of the tile being computed)
+    int32_t* rowok = dbg_row + (DBG ? Geo::KV_ROWS + Geo::Q_ROWS : 0);
+    int32_t* pt_lds = rowok + 2 * Geo::KV_ROWS;
+    int par = 0;
     const Divider gdiv = sa.gdiv;
+    if constexpr (PAGED) {
+        // the page table, before anything else: the first tile's loads need it
+        // (the barrier below the first tile's setup publishes it)
+        const int npt = p.B * p.pt_cols;
+        for (int i = threadIdx.x; i < npt; i += kStThreads) pt_lds[i] = p.page_table[i];
+    }
 
     const int grp = divide((int)blockIdx.x, sa.ngroups);
     const int g = (int)blockIdx.x - grp * sa.ngroups.d;  // group
@@ -752,9 +812,10 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void tree_stream_kernel(
         lvl_lds[threadIdx.x] = lvl_st0;
         lvl_lds[64 + threadIdx.x] = (int32_t)lvl_pw0;
     }
+    if constexpr (PAGED) __syncthreads();  // the LDS page table
     if (cur.valid) {
         tile_rowmap<D>(p, gdiv, cur, rm);
-        tile_issue<D, BATCH>(p, cur, rm, sg);
+        tile_issue<D, BATCH, PAGED>(p, cur, rm, sg, pt_lds, rowok);
         // the first query table is built while the first loads are in flight
         // (the first loop top's barrier publishes it)
         build_query_table(p, gdiv, cur, qtab);
@@ -783,7 +844,7 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void tree_stream_kernel(
             const bool fresh = tile_setup<D>(p, plan, sa, cu_lds, wn, cur, nxt, band_tb, band_pk, lvl_lds);
             if (nxt.valid) {
                 if (fresh) tile_rowmap<D>(p, gdiv, nxt, rm);
-                tile_issue<D, BATCH>(p, nxt, rm, sg);
+                tile_issue<D, BATCH, PAGED>(p, nxt, rm, sg, pt_lds, rowok + (par ^ 1) * Geo::KV_ROWS);
             }
         }
         // the next item, or (after this workgroup's last request) done
@@ -796,13 +857,17 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void tree_stream_kernel(
                 tab_n = cur.n;
                 __syncthreads();
             }
-            if constexpr (DBG) dbg_walk_export(p, cur, qtab, dbg_row, dbg_q);
-            tile_compute<T, D, LSE, PSTATE, BATCH>(p, cur, Ks, Vs, Qs, qtab);
+            // the rows that exist: all, or (paged) those whose page does
+            uint64_t vmask = ~uint64_t(0);
+            if constexpr (PAGED) vmask = __ballot(lane < Geo::KV_ROWS && rowok[par * Geo::KV_ROWS + lane] != 0);
+            if constexpr (DBG) dbg_walk_export(p, cur, qtab, dbg_row, dbg_q, vmask);
+            tile_compute<T, D, LSE, PSTATE, BATCH>(p, cur, Ks, Vs, Qs, qtab, vmask);
         }
         __syncthreads();
         if (!more) break;
         cur = nxt;
         k = kn;
+        par ^= 1;
     }
     // The last workgroup of the group to finish clears its counters: every
     // other one has made its last request before adding to done_ctr.
@@ -894,7 +959,7 @@ static uint32_t* sched_counters(int dev, hipStream_t st) {
     return sd.pool + 2 * slot;
 }
 
-template <typename T, int D, bool LSE, bool PSTATE, bool BATCH, bool DBG = false>
+template <typename T, int D, bool LSE, bool PSTATE, bool BATCH, bool DBG = false, bool PAGED = false>
 static int launch_stream_t(const TreeParams& p, const SubtreePlan& plan, hipStream_t st) {
     using Geo = StreamGeom<D>;
     const int64_t n_work = (int64_t)p.B * p.Hkv * plan.total_tiles;
@@ -907,8 +972,14 @@ static int launch_stream_t(const TreeParams& p, const SubtreePlan& plan, hipStre
         set_error("subtree kernel: batch %d exceeds %d sequences", p.B, kCuCache - 1);
         return QATTN_ERR_ARG;
     }
-    const size_t lds = Geo::LDS_BYTES + (DBG ? Geo::DBG_BYTES : 0);
-    auto kern = tree_stream_kernel<T, D, LSE, PSTATE, BATCH, DBG>;
+    const int64_t npt = PAGED ? (int64_t)p.B * p.pt_cols : 0;
+    if (PAGED && (npt > kPtCache || !p.page_table || p.page_size < 1)) {
+        set_error("subtree kernel: page table of %lld entries exceeds %d", (long long)npt, kPtCache);
+        return QATTN_ERR_ARG;
+    }
+    const size_t lds = Geo::LDS_BYTES + (DBG ? Geo::DBG_BYTES : 0) +
+                       (PAGED ? Geo::ROWOK_BYTES + (size_t)npt * 4 : 0);
+    auto kern = tree_stream_kernel<T, D, LSE, PSTATE, BATCH, DBG, PAGED>;
     int dev = 0, cus = 0, per_cu = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
@@ -943,16 +1014,21 @@ static int launch_stream_t(const TreeParams& p, const SubtreePlan& plan, hipStre
     return launch_status("tree_stream_kernel");
 }
 
-int launch_stream(const TreeParams& p, const SubtreePlan& plan, int dtype, int head_dim, bool pstate,
+int launch_stream(const TreeParams& p, const SubtreePlan& plan, int dtype, int head_dim, bool pstate, bool paged,
                   hipStream_t st) {
+    if (paged && (pstate || !p.cu)) {
+        set_error("the paged subtree kernel takes packed cu_seqlens and no prefix state");
+        return QATTN_ERR_ARG;
+    }
     if (p.dbg_walk) {
-        // walk export: fp16, packed layout, no LSE (the walk does not depend on them)
+        // walk export: fp16, packed cu_seqlens, no LSE (the walk does not depend on them)
         if (dtype != QATTN_DTYPE_F16 || p.lse || !p.cu) {
             set_error("the walk export runs fp16 calls over packed cu_seqlens without LSE");
             return QATTN_ERR_ARG;
         }
-#define QATTN_STREAM_DBG(D) \
-    return pstate ? launch_stream_t<F16, D, false, true, false, true>(p, plan, st) \
+#define QATTN_STREAM_DBG(D)                                                                        \
+    if (paged) return launch_stream_t<F16, D, false, false, false, true, true>(p, plan, st);       \
+    return pstate ? launch_stream_t<F16, D, false, true, false, true>(p, plan, st)                  \
                   : launch_stream_t<F16, D, false, false, false, true>(p, plan, st);
         if (head_dim == 32) { QATTN_STREAM_DBG(32) }
         if (head_dim == 64) { QATTN_STREAM_DBG(64) }
@@ -964,8 +1040,10 @@ int launch_stream(const TreeParams& p, const SubtreePlan& plan, int dtype, int h
                              : launch_stream_t<T, D, true, false, B>(p, plan, st);              \
     return pstate ? launch_stream_t<T, D, false, true, B>(p, plan, st)                          \
                   : launch_stream_t<T, D, false, false, B>(p, plan, st);
-#define QATTN_STREAM_D(T, D)               \
-    if (!p.cu) { QATTN_STREAM_B(T, D, true) } \
+#define QATTN_STREAM_D(T, D)                                                                   \
+    if (paged) return p.lse ? launch_stream_t<T, D, true, false, false, false, true>(p, plan, st)   \
+                            : launch_stream_t<T, D, false, false, false, false, true>(p, plan, st); \
+    if (!p.cu) { QATTN_STREAM_B(T, D, true) }                                                     \
     QATTN_STREAM_B(T, D, false)
     if (dtype == QATTN_DTYPE_F16) {
         if (head_dim == 32) { QATTN_STREAM_D(F16, 32) }

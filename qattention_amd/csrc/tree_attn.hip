@@ -335,11 +335,14 @@ static int gather_packed(const TreeParams& p, bool lse, bool pstate, hipStream_t
 template <typename T, int D>
 static int dispatch_tree(const TreeParams& p, int walk, int layout, bool lse, bool pstate, int algo,
                          hipStream_t st) {
-    if (walk == WALK_HEAP && layout == KV_PACKED && algo != QATTN_ALGO_GATHER) {
+    const bool paged = layout == KV_PAGED;
+    if (walk == WALK_HEAP && (!paged || !pstate) && algo != QATTN_ALGO_GATHER) {
         SubtreePlan plan;
         int rcap = 0, qcap = 0;
         stream_tile_caps(D, &rcap, &qcap);
+        // (paged: the page table is copied to LDS, so it has a size limit)
         const bool ok = p.B <= stream_max_batch() &&
+                        (!paged || (int64_t)p.B * p.pt_cols <= stream_max_page_entries()) &&
                         make_subtree_plan(p.bdiv.d, p.max_seqlen, p.max_depth, rcap, qcap / p.group, plan);
         const int64_t wgs = ok ? (int64_t)p.B * p.Hkv * plan.total_tiles : 0;
         // The subtree kernel needs enough tiles to fill 256 CUs; a merged
@@ -347,13 +350,13 @@ static int dispatch_tree(const TreeParams& p, int walk, int layout, bool lse, bo
         // when tiles are plentiful.
         const bool use = ok && (algo == QATTN_ALGO_SUBTREE || wgs >= (pstate ? 2048 : 512));
         if (algo == QATTN_ALGO_SUBTREE && !ok) {
-            set_error("no subtree plan fits (b=%d, max_seqlen=%d, max_depth=%d, batch=%d)", p.bdiv.d,
-                      p.max_seqlen, p.max_depth, p.B);
+            set_error("no subtree plan fits (b=%d, max_seqlen=%d, max_depth=%d, batch=%d, page-table entries %lld)",
+                      p.bdiv.d, p.max_seqlen, p.max_depth, p.B, paged ? (long long)p.B * p.pt_cols : 0LL);
             return QATTN_ERR_ARG;
         }
-        if (use) return launch_stream(p, plan, T::kCode, D, pstate, st);
+        if (use) return launch_stream(p, plan, T::kCode, D, pstate, paged, st);
     } else if (algo == QATTN_ALGO_SUBTREE) {
-        set_error("the subtree kernel supports the heap walk on packed K/V only");
+        set_error("the subtree kernel supports the heap walk on packed or paged K/V only");
         return QATTN_ERR_ARG;
     }
     if (p.dbg_walk) {
@@ -527,10 +530,14 @@ int qattn_tree_paged_fwd(const void* q, const int64_t q_stride[3], const void* k
                          const int32_t* page_table, int32_t pt_cols, int32_t num_pages, int32_t page_size,
                          int32_t batch, int32_t max_seqlen, int64_t total_tokens, int32_t num_q_heads,
                          int32_t num_kv_heads, int32_t head_dim, int32_t branching_factor, int32_t max_depth,
-                         float scale, int32_t dtype, void* stream) {
+                         float scale, int32_t dtype, int32_t algo, void* stream) {
     clear_error();
     int rc = check_common(dtype, head_dim, batch, max_seqlen, total_tokens, num_q_heads, num_kv_heads, max_depth);
     if (rc) return rc;
+    if (algo < QATTN_ALGO_AUTO || algo > QATTN_ALGO_SUBTREE) {
+        set_error("unknown algo %d", algo);
+        return QATTN_ERR_ARG;
+    }
     if (batch == 0 || max_seqlen == 0 || total_tokens == 0) return QATTN_OK;  // nothing to compute
     if (!page_table || !k_stride || !v_stride || page_size < 1 || pt_cols < 0 || num_pages < 0) {
         set_error("bad paged arguments: page_size=%d pt_cols=%d num_pages=%d", page_size, pt_cols, num_pages);
@@ -552,9 +559,10 @@ int qattn_tree_paged_fwd(const void* q, const int64_t q_stride[3], const void* k
     p.pt_cols = pt_cols;
     p.num_pages = num_pages;
     p.page_size = page_size;
+    p.pdiv = make_divider(page_size);
     p.sk_page = k_stride[0];
     p.sv_page = v_stride[0];
-    return run_tree(p, dtype, head_dim, WALK_HEAP, KV_PAGED, false, QATTN_ALGO_GATHER, (hipStream_t)stream);
+    return run_tree(p, dtype, head_dim, WALK_HEAP, KV_PAGED, false, algo, (hipStream_t)stream);
 }
 
 int qattn_ancestors(const int32_t* cu_seqlens, const int32_t* parents, int32_t batch, int32_t max_seqlen,

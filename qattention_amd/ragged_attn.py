@@ -273,6 +273,15 @@ def ragged_attention_paged(
     K_cache/V_cache: [pages, PAGE_SIZE, Hkv, D]; page_table: [B, max_pages]
     int32 logical->physical page map; ancestor position c of sequence b is
     slot c % PAGE_SIZE of page page_table[b, c // PAGE_SIZE]."""
+    return _paged_forward(Q, K_cache, V_cache, page_table, cu_seqlens, branching_factor, max_depth, max_seqlen,
+                          False)[0]
+
+
+def _paged_forward(Q, K_cache, V_cache, page_table, cu_seqlens, branching_factor, max_depth, max_seqlen,
+                   want_lse: bool, algo: int = _lib.ALGO_AUTO):
+    """ragged_attention_paged with an optional LSE ([T, Hq] fp32; -inf for a
+    query that attends nothing) and a kernel choice (tests time and check
+    both kernels)."""
     assert K_cache.shape == V_cache.shape, "K and V cache shapes must match"
     _check_dtypes(Q, K_cache, V_cache)
     device = _require_device(Q, K_cache, V_cache)
@@ -289,16 +298,18 @@ def ragged_attention_paged(
     O = torch.empty_like(Q)
     if not _vec_ok(O):
         O = torch.empty(Q.shape, dtype=Q.dtype, device=device)
+    lse = torch.empty(T, Hq, dtype=torch.float32, device=device) if want_lse else None
     L = _lib.lib()
     with torch.cuda.device(device):
         rc = L.qattn_tree_paged_fwd(
             Q.data_ptr(), _lib.i64arr(Q.stride()), K_cache.data_ptr(), _lib.i64arr(K_cache.stride()),
             V_cache.data_ptr(), _lib.i64arr(V_cache.stride()), O.data_ptr(), _lib.i64arr(O.stride()),
-            None, None, cu_dev.data_ptr(), pt.data_ptr(), int(pt.stride(0)), num_pages, page_size,
+            lse.data_ptr() if want_lse else None, _lib.i64arr(lse.stride()) if want_lse else None,
+            cu_dev.data_ptr(), pt.data_ptr(), int(pt.stride(0)), num_pages, page_size,
             B, ms, T, Hq, Hkv, D, int(branching_factor), int(max_depth), 1.0 / math.sqrt(D),
-            _dtype_code(Q), _stream(device))
+            _dtype_code(Q), int(algo), _stream(device))
     _lib.check(rc, "qattn_tree_paged_fwd")
-    return O
+    return O, lse
 
 
 def build_paged_kv(

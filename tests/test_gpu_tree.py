@@ -390,9 +390,89 @@ def test_paged(page_size):
     inv[perm] = torch.arange(perm.numel())
     Kc, Vc = Kc[perm.to(DEV)].contiguous(), Vc[perm.to(DEV)].contiguous()
     pt = inv[pt.long()].to(torch.int32)
-    o_ref, _, _ = oracle_tree(Q, K, V, cu, 4, 3)
+    o_ref, lse_ref, _ = oracle_tree(Q, K, V, cu, 4, 3)
     O = ra.ragged_attention_paged(Q.to(DEV), Kc, Vc, pt, cu, 4, 3)
     check_fp16(O.double().cpu().numpy(), o_ref, "paged")
+    # both kernels, with the LSE
+    for algo in (_lib_algo("gather"), _lib_algo("subtree")):
+        O, L = ra._paged_forward(Q.to(DEV), Kc, Vc, pt, cu, 4, 3, None, True, algo)
+        check_fp16(O.double().cpu().numpy(), o_ref, f"paged algo {algo}")
+        assert np.abs(L.double().cpu().numpy() - lse_ref).max() <= 1e-4, f"paged LSE algo {algo}"
+
+
+def _lib_algo(name):
+    _, lib = _ra()
+    return {"auto": lib.ALGO_AUTO, "gather": lib.ALGO_GATHER, "subtree": lib.ALGO_SUBTREE}[name]
+
+
+def _shuffled_paged(ra, K, V, cu, H, page_size, seed):
+    """build_paged_kv over the packed K/V, physical pages in a shuffled order."""
+    cuL = cu.tolist()
+    B = len(cuL) - 1
+    ks = [K[cuL[i]:cuL[i + 1]].to(DEV) for i in range(B)]
+    vs = [V[cuL[i]:cuL[i + 1]].to(DEV) for i in range(B)]
+    Kc, Vc, pt = ra.build_paged_kv(ks, vs, page_size=page_size)
+    perm = torch.randperm(Kc.shape[0], generator=torch.Generator().manual_seed(seed))
+    inv = torch.empty_like(perm)
+    inv[perm] = torch.arange(perm.numel())
+    return Kc[perm.to(DEV)].contiguous(), Vc[perm.to(DEV)].contiguous(), inv[pt.long()].to(torch.int32)
+
+
+# (lens, b, max_depth, Hq, Hkv, D, page_size): the subtree kernel on paged K/V
+# -- cfg2's trees, pages of 1, 5 (not a power of two), 16 and 4096 (one page
+# per sequence), bf16-sized heads, GQA, ragged and empty sequences
+PAGED_SUBTREE_CASES = [
+    ([1365] * 2, 4, 5, 8, 8, 128, 16),
+    ([1365, 300], 4, 5, 4, 4, 128, 5),
+    ([121, 0, 40, 1], 3, 4, 8, 2, 128, 1),
+    ([1023], 2, 9, 4, 4, 64, 16),
+    ([700, 33], 4, 2, 6, 3, 32, 4096),
+]
+
+
+@pytest.mark.parametrize("lens,b,md,Hq,Hkv,D,ps", PAGED_SUBTREE_CASES)
+def test_paged_subtree(lens, b, md, Hq, Hkv, D, ps):
+    """The paged subtree kernel against the oracle and the paged gather kernel
+    (same cache, same page table): O within the fp16 bound, LSE 1e-4."""
+    ra, _ = _ra()
+    say("paged subtree", lens[:4], b, md, Hq, Hkv, D, ps)
+    Q, K, V, cu = make_inputs(lens, Hq, D, 2100 + ps, Hkv=Hkv)
+    Kc, Vc, pt = _shuffled_paged(ra, K, V, cu, Hkv, ps, 7)
+    o_ref, lse_ref, _ = oracle_tree(Q, K, V, cu, b, md)
+    Qd = Q.to(DEV)
+    for algo in (_lib_algo("subtree"), _lib_algo("gather")):
+        O, L = ra._paged_forward(Qd, Kc, Vc, pt, cu, b, md, None, True, algo)
+        torch.cuda.synchronize()
+        check_fp16(O.double().cpu().numpy(), o_ref, f"paged algo {algo}")
+        assert np.abs(L.double().cpu().numpy() - lse_ref).max() <= 1e-4, f"paged LSE algo {algo}"
+
+
+def test_paged_subtree_bf16():
+    ra, _ = _ra()
+    say("paged subtree bf16")
+    lens, b, md = [1365, 85], 4, 5
+    Q, K, V, cu = make_inputs(lens, 8, 128, 2150, dtype=torch.bfloat16, Hkv=4)
+    Kc, Vc, pt = _shuffled_paged(ra, K, V, cu, 4, 16, 9)
+    o_ref, _, _ = oracle_tree(Q, K, V, cu, b, md)
+    O, _ = ra._paged_forward(Q.to(DEV), Kc, Vc, pt, cu, b, md, None, False, _lib_algo("subtree"))
+    check_bf16(O.float().double().cpu().numpy(), o_ref, "paged subtree bf16")
+
+
+def test_paged_subtree_table_limit():
+    """A page table of more than 2048 entries: the automatic choice runs the
+    gather kernel (same results), the forced subtree kernel is an error."""
+    ra, lib = _ra()
+    say("paged table limit")
+    lens, b, md = [121] * 3, 3, 4
+    Q, K, V, cu = make_inputs(lens, 4, 64, 2160)
+    Kc, Vc, pt = _shuffled_paged(ra, K, V, cu, 4, 16, 3)
+    wide = torch.full((3, 700), -1, dtype=torch.int32)  # 2100 entries
+    wide[:, :pt.shape[1]] = pt
+    o_ref, _, _ = oracle_tree(Q, K, V, cu, b, md)
+    O, _ = ra._paged_forward(Q.to(DEV), Kc, Vc, wide, cu, b, md, None, False, lib.ALGO_AUTO)
+    check_fp16(O.double().cpu().numpy(), o_ref, "paged, wide table")
+    with pytest.raises(lib.QAttnError, match="page-table entries"):
+        ra._paged_forward(Q.to(DEV), Kc, Vc, wide, cu, b, md, None, False, lib.ALGO_SUBTREE)
 
 
 def test_paged_missing_pages():
@@ -422,17 +502,27 @@ def test_paged_missing_pages():
                 if page < 0 or page >= Kc.shape[0]:
                     anc[t, s1] = -1
     assert (anc[:cuL[1]] < 0).all(axis=1).any()  # some query attends nothing
-    o_ref, _ = clib.tree_attn(Q.float().numpy(), K.float().numpy(), V.float().numpy(), cu.numpy(), anc,
-                              1.0 / 8.0)
+    o_ref, lse_ref = clib.tree_attn(Q.float().numpy(), K.float().numpy(), V.float().numpy(), cu.numpy(), anc,
+                                    1.0 / 8.0)
     O = ra.ragged_attention_paged(Q.to(DEV), Kc, Vc, pt, cu, b, d)
     check_fp16(O.double().cpu().numpy(), o_ref, "paged, missing pages")
+    empty = np.isneginf(lse_ref)
+    assert empty.any()
+    for algo in (_lib_algo("gather"), _lib_algo("subtree")):
+        O, L = ra._paged_forward(Q.to(DEV), Kc, Vc, pt, cu, b, d, None, True, algo)
+        check_fp16(O.double().cpu().numpy(), o_ref, f"paged, missing pages, algo {algo}")
+        L = L.double().cpu().numpy()
+        assert (np.isneginf(L) == empty).all(), f"algo {algo}: LSE -inf exactly where nothing is attended"
+        assert np.abs(L[~empty] - lse_ref[~empty]).max() <= 1e-4, f"algo {algo}: LSE"
 
 
-def test_paged_graph_capture_replay():
+@pytest.mark.parametrize("algo", ["gather", "subtree"])
+def test_paged_graph_capture_replay(algo):
     """With max_seqlen (and device cu / page table) the paged call makes no
     host read and records into a HIP graph; replays after new cache contents
     are copied in match eager calls on the same contents."""
     ra, _ = _ra()
+    code = _lib_algo(algo)
     b, d, N, B, ps = 3, 4, 121, 3, 16
     Q, K, V, cu = make_inputs([N] * B, 8, 128, 2040, Hkv=4)
     Kc, Vc, pt = ra.build_paged_kv(list(K.to(DEV).view(B, N, 4, 128)), list(V.to(DEV).view(B, N, 4, 128)), ps)
@@ -440,11 +530,11 @@ def test_paged_graph_capture_replay():
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
-        ra.ragged_attention_paged(Qd, Kc, Vc, ptd, cud, b, d, max_seqlen=N)
+        ra._paged_forward(Qd, Kc, Vc, ptd, cud, b, d, N, False, code)
     torch.cuda.current_stream().wait_stream(s)
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
-        out = ra.ragged_attention_paged(Qd, Kc, Vc, ptd, cud, b, d, max_seqlen=N)
+        out, _ = ra._paged_forward(Qd, Kc, Vc, ptd, cud, b, d, N, False, code)
     g = torch.Generator().manual_seed(2041)
     for i in range(3):
         Kc.copy_(torch.randn(Kc.shape, generator=g).half())
@@ -453,7 +543,7 @@ def test_paged_graph_capture_replay():
         torch.cuda.synchronize()
         graph.replay()
         torch.cuda.synchronize()
-        eager = ra.ragged_attention_paged(Qd, Kc, Vc, ptd, cud, b, d, max_seqlen=N)
+        eager, _ = ra._paged_forward(Qd, Kc, Vc, ptd, cud, b, d, N, False, code)
         torch.cuda.synchronize()
         assert torch.equal(out, eager), f"replay {i}"
 

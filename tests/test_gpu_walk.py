@@ -135,12 +135,15 @@ def test_parents_walk_bitexact(lens, md, window):
     _check_out(O, o_ref, "parents outputs")
 
 
-def test_paged_walk_bitexact():
-    """The paged gather walk: 16-token pages in a shuffled physical order,
-    one logical page missing from the table (its ancestors are skipped)."""
+@pytest.mark.parametrize("algo", ["subtree", "gather"])
+def test_paged_walk_bitexact(algo):
+    """The paged walk of both kernels: 16-token pages in a shuffled physical
+    order, one logical page missing from the table (its ancestors are
+    skipped); the outputs of the same call match the oracle on that table."""
     ra, _lib = _mods()
     lens, b, md, H, D = [1365, 341], 4, 5, 8, 128
-    say("walk paged")
+    say("walk paged", algo)
+    code = _lib.ALGO_SUBTREE if algo == "subtree" else _lib.ALGO_GATHER
     Q, K, V, cu = make_inputs(lens, H, D, 4200)
     Kc, Vc, pt = ra.build_paged_kv([K[:1365], K[1365:]], [V[:1365], V[1365:]], 16)
     g = torch.Generator().manual_seed(4201)
@@ -152,12 +155,15 @@ def test_paged_walk_bitexact():
     T = Q.shape[0]
     table = _table(T, H, md)
     with _lib.debug_walk(table):
-        ra.ragged_attention_paged(Q.to(DEV), Kp.to(DEV), Vp.to(DEV), ptp, cu, b, md)
+        O, _ = ra._paged_forward(Q.to(DEV), Kp.to(DEV), Vp.to(DEV), ptp, cu, b, md, None, False, code)
     torch.cuda.synchronize()
     ref = clib.ancestor_table_heap(cu.numpy(), b, md)
     seq1 = ref[1365:]
     seq1[(seq1 >= 48) & (seq1 < 64)] = -1  # missing page: those ancestors are not attended
-    _expect(table, ref, "paged walk")
+    _expect(table, ref, f"{algo} paged walk")
+    o_ref, _ = clib.tree_attn(Q.float().numpy(), K.float().numpy(), V.float().numpy(), cu.numpy(), ref,
+                              1.0 / math.sqrt(D), want_lse=False)
+    _check_out(O, o_ref, f"{algo} paged outputs")
 
 
 def _prefix(B, L, Hkv, D, seed):

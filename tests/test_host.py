@@ -103,7 +103,11 @@ def test_abi_validation_other_entry_points():
     assert L.qattn_tree_parents_fwd(FAKE, ok3, FAKE, ok3, FAKE, ok3, FAKE, ok3, FAKE, _lib.i64arr((4, 1)),
                                     FAKE, None, 1, 15, 15, 4, 4, 64, 3, 0.125, 0, None) == -1
     assert L.qattn_tree_paged_fwd(FAKE, ok3, FAKE, ok4, FAKE, ok4, FAKE, ok3, None, None, FAKE, FAKE,
-                                  4, 4, 0, 1, 15, 15, 4, 4, 64, 2, 3, 0.125, 0, None) == -1
+                                  4, 4, 0, 1, 15, 15, 4, 4, 64, 2, 3, 0.125, 0, 0, None) == -1
+    ok_pt = (FAKE, ok3, FAKE, ok4, FAKE, ok4, FAKE, ok3, None, None, FAKE, FAKE, 4, 4, 16, 1, 15, 15, 4, 4, 64, 2, 3,
+             0.125, 0)
+    assert L.qattn_tree_paged_fwd(*ok_pt, 3, None) == -1  # unknown algo
+    assert "algo" in _lib.last_error()
     assert L.qattn_ancestors(FAKE, None, 1, 15, 15, 0, 3, FAKE, None) == -1
     s3 = _lib.i64arr((60, 15, 1))
     assert L.qattn_lse_merge(FAKE, s3, FAKE, s3, FAKE, ok4, FAKE, ok4, FAKE, ok4, 1, 4, 15, 48, 0, None) == -3
