@@ -278,7 +278,12 @@ __device__ __forceinline__ bool tile_setup(const TreeParams& p, const SubtreePla
 // wave works out K/V row x and Q row x of the tile (one pass over the levels
 // with wave-uniform values: row x lies in the last level whose base is <= x),
 // then every thread takes the rows it stages from those lanes.
-template <int D>
+// PAGED: kvrow holds the row's logical page << kSlotBits | its slot in the
+// page instead of its node (the host keeps page_size <= 2^kSlotBits and the
+// logical pages below 2^(31 - kSlotBits)), so the tile loop needs neither
+// the page size nor its divider.
+constexpr int kSlotBits = 12;
+template <int D, bool PAGED = false>
 __device__ __forceinline__ void tile_rowmap(const TreeParams& p, const Divider& gdiv, const TileMeta& t,
                                             RowMap<D>& rm) {
     using Geo = StreamGeom<D>;
@@ -301,7 +306,11 @@ __device__ __forceinline__ void tile_rowmap(const TreeParams& p, const Divider& 
     }
     const int sq = x - qbl;
     const int nd = divide(sq, gdiv);
-    const int kvnode = x - koff;                                  // K/V row x: node, relative to the tile's kv base
+    int kvnode = x - koff;                                        // K/V row x: node, relative to the tile's kv base
+    if constexpr (PAGED) {
+        const int lp = divide(kvnode, p.pdiv);  // kvnode >= 0
+        kvnode = (lp << kSlotBits) | (kvnode - lp * p.page_size);
+    }
     const int qpack = ((fl + nd) << 8) | (sq - nd * p.group);     // Q row x: node << 8 | q head in the group
     const int rsub = (threadIdx.x + z) / Geo::CPR;
 #pragma unroll
@@ -315,8 +324,9 @@ __device__ __forceinline__ void tile_rowmap(const TreeParams& p, const Divider& 
 // Issue the global loads of a tile into the staging registers.
 // PAGED: node x of the sequence lives in slot x % page_size of page
 // pt[seq][x / page_size] (src/ragged_attn.py:822-929); pt_lds is the
-// workgroup's LDS copy of the page table.  A row whose logical page is past
-// pt_cols or whose page is outside [0, num_pages) gets flag 0 in rowok (this
+// workgroup's LDS copy of the page table, in which a page outside
+// [0, num_pages) reads -1.  A row whose logical page is past pt_cols or
+// whose page is missing gets flag 0 in rowok (this
 // tile's half of the double buffer; the compute masks the row out) and reads
 // the tile's first Q row instead (in bounds, and finite whenever an output
 // can be: P = 0 multiplies its V, the mask replaces its score).  Loads stay
@@ -334,7 +344,7 @@ __device__ __forceinline__ void tile_issue(const TreeParams& p, const TileMeta& 
     const int c8 = 8 * ((threadIdx.x + z) % Geo::CPR);
     const int64_t kvb = PAGED ? 0 : t.kvb;
     const uint16_t* kg = (const uint16_t*)p.k + (kvb * p.sk_t + (int64_t)t.kvh * p.sk_h + c8);
-    const uint16_t* vg = (const uint16_t*)p.v + (kvb * p.sv_t + (int64_t)t.kvh * p.sv_h + c8);
+    const uint16_t* vg = (const uint16_t*)p.v + (kvb * p.sv_t + (int64_t)t.kvh * (PAGED ? p.sk_h : p.sv_h) + c8);
     const uint16_t* qg =
         (const uint16_t*)p.q +
         ((int64_t)t.start * p.sq_t + (BATCH ? (int64_t)t.seq * p.sq_b : 0) + (int64_t)t.kvh * p.group * p.sq_h + c8);
@@ -346,14 +356,15 @@ __device__ __forceinline__ void tile_issue(const TreeParams& p, const TileMeta& 
             if (ps * Geo::RPP >= t.rows) break;  // wave-uniform
             const int r = ps * Geo::RPP + rsub;
             if (r < t.rows) {
-                const int32_t node = rm.kvrow[ps];
-                const int32_t lp = divide(node, p.pdiv);
-                const int32_t slot = node - lp * p.page_size;
+                const int32_t lp = rm.kvrow[ps] >> kSlotBits;
+                const int32_t slot = rm.kvrow[ps] & ((1 << kSlotBits) - 1);
                 const int32_t pg = lp < p.pt_cols ? ptrow[lp] : -1;
-                const bool ok = (uint32_t)pg < (uint32_t)p.num_pages;
+                const bool ok = pg >= 0;
                 if (c0) rowok[r] = ok ? 1 : 0;
-                const uint16_t* kr = ok ? kg + (int64_t)pg * p.sk_page + (int64_t)slot * p.sk_t : qg;
-                const uint16_t* vr = ok ? vg + (int64_t)pg * p.sv_page + (int64_t)slot * p.sv_t : qg;
+                const uint64_t off = (uint64_t)(uint32_t)pg * (uint32_t)p.sk_page +
+                                     (uint64_t)(uint32_t)slot * (uint32_t)p.sk_t;
+                const uint16_t* kr = ok ? kg + off : qg;
+                const uint16_t* vr = ok ? vg + off : qg;
                 sg.k[ps] = ld16(kr);
                 sg.v[ps] = ld16(vr);
             }
@@ -379,9 +390,9 @@ __device__ __forceinline__ void tile_issue(const TreeParams& p, const TileMeta& 
 // Write the staged tile to LDS (K, V and Q rows at the padded pitch).  V rows
 // past the tile's last row keep the previous tile's (finite) values or the
 // zeros written at kernel start; P = 0 multiplies them.
-template <int D, bool DBG = false>
-__device__ __forceinline__ void tile_store(const TileMeta& t, uint16_t* Ks, uint16_t* Vs, uint16_t* Qs,
-                                           const Stage<D>& sg, const RowMap<D>& rm, int32_t* dbg_row,
+template <int D, bool DBG = false, bool PAGED = false>
+__device__ __forceinline__ void tile_store(const TreeParams& p, const TileMeta& t, uint16_t* Ks, uint16_t* Vs,
+                                           uint16_t* Qs, const Stage<D>& sg, const RowMap<D>& rm, int32_t* dbg_row,
                                            int32_t* dbg_q) {
     using Geo = StreamGeom<D>;
     const int tid = threadIdx.x;
@@ -393,7 +404,10 @@ __device__ __forceinline__ void tile_store(const TileMeta& t, uint16_t* Ks, uint
 #pragma unroll
             for (int ps = 0; ps < Geo::PASSES; ++ps) {
                 const int r = ps * Geo::RPP + rsub;
-                dbg_row[r] = r < t.rows ? rm.kvrow[ps] : -1;
+                dbg_row[r] = r < t.rows ? (PAGED ? (rm.kvrow[ps] >> kSlotBits) * p.page_size +
+                                                       (rm.kvrow[ps] & ((1 << kSlotBits) - 1))
+                                                 : rm.kvrow[ps])
+                                        : -1;
                 dbg_q[r] = r < t.nq ? rm.qrow[ps] : -1;
             }
         }
@@ -750,9 +764,15 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void tree_stream_kernel(
     const Divider gdiv = sa.gdiv;
     if constexpr (PAGED) {
         // the page table, before anything else: the first tile's loads need it
-        // (the barrier below the first tile's setup publishes it)
+        // (the barrier below the first tile's setup publishes it); missing
+        // pages become -1 here, once, so the tile loop does not test them.
+        // (Staging these loads in registers, or issuing four before the
+        // stores, measured slower.)
         const int npt = p.B * p.pt_cols;
-        for (int i = threadIdx.x; i < npt; i += kStThreads) pt_lds[i] = p.page_table[i];
+        for (int i = threadIdx.x; i < npt; i += kStThreads) {
+            const int32_t e = p.page_table[i];
+            pt_lds[i] = (uint32_t)e < (uint32_t)p.num_pages ? e : -1;
+        }
     }
 
     const int grp = divide((int)blockIdx.x, sa.ngroups);
@@ -814,7 +834,7 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void tree_stream_kernel(
     }
     if constexpr (PAGED) __syncthreads();  // the LDS page table
     if (cur.valid) {
-        tile_rowmap<D>(p, gdiv, cur, rm);
+        tile_rowmap<D, PAGED>(p, gdiv, cur, rm);
         tile_issue<D, BATCH, PAGED>(p, cur, rm, sg, pt_lds, rowok);
         // the first query table is built while the first loads are in flight
         // (the first loop top's barrier publishes it)
@@ -833,7 +853,7 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void tree_stream_kernel(
         __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
         if (first && threadIdx.x <= p.B) cuc[threadIdx.x] = cu_mine;
         first = false;
-        if (cur.valid) tile_store<D, DBG>(cur, Ks, Vs, Qs, sg, rm, dbg_row, dbg_q);
+        if (cur.valid) tile_store<D, DBG, PAGED>(p, cur, Ks, Vs, Qs, sg, rm, dbg_row, dbg_q);
         if (leader) *next_slot = dyn ? sa.gsize + (int)ans : k + sa.gsize;
         __syncthreads();
         const int kn = __builtin_amdgcn_readfirstlane(*next_slot);
@@ -843,7 +863,7 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void tree_stream_kernel(
         if (more) {
             const bool fresh = tile_setup<D>(p, plan, sa, cu_lds, wn, cur, nxt, band_tb, band_pk, lvl_lds);
             if (nxt.valid) {
-                if (fresh) tile_rowmap<D>(p, gdiv, nxt, rm);
+                if (fresh) tile_rowmap<D, PAGED>(p, gdiv, nxt, rm);
                 tile_issue<D, BATCH, PAGED>(p, nxt, rm, sg, pt_lds, rowok + (par ^ 1) * Geo::KV_ROWS);
             }
         }

@@ -340,9 +340,14 @@ static int dispatch_tree(const TreeParams& p, int walk, int layout, bool lse, bo
         SubtreePlan plan;
         int rcap = 0, qcap = 0;
         stream_tile_caps(D, &rcap, &qcap);
-        // (paged: the page table is copied to LDS, so it has a size limit)
-        const bool ok = p.B <= stream_max_batch() &&
-                        (!paged || (int64_t)p.B * p.pt_cols <= stream_max_page_entries()) &&
+        // (paged: the page table is copied to LDS, so it has a size limit, and
+        // one 32-bit offset addresses K and V: equal strides below 2^31)
+        const bool paged_ok = !paged || ((int64_t)p.B * p.pt_cols <= stream_max_page_entries() &&
+                                         p.sk_page == p.sv_page && p.sk_t == p.sv_t && p.sk_h == p.sv_h &&
+                                         p.sk_page >= 0 && p.sk_page < (int64_t(1) << 31) && p.sk_t >= 0 &&
+                                         p.sk_t < (int64_t(1) << 31) && p.page_size <= 4096 &&
+                                         (p.max_seqlen - 1) / p.page_size < (1 << 19));
+        const bool ok = p.B <= stream_max_batch() && paged_ok &&
                         make_subtree_plan(p.bdiv.d, p.max_seqlen, p.max_depth, rcap, qcap / p.group, plan);
         const int64_t wgs = ok ? (int64_t)p.B * p.Hkv * plan.total_tiles : 0;
         // The subtree kernel needs enough tiles to fill 256 CUs; a merged
@@ -350,8 +355,13 @@ static int dispatch_tree(const TreeParams& p, int walk, int layout, bool lse, bo
         // when tiles are plentiful.
         const bool use = ok && (algo == QATTN_ALGO_SUBTREE || wgs >= (pstate ? 2048 : 512));
         if (algo == QATTN_ALGO_SUBTREE && !ok) {
-            set_error("no subtree plan fits (b=%d, max_seqlen=%d, max_depth=%d, batch=%d, page-table entries %lld)",
-                      p.bdiv.d, p.max_seqlen, p.max_depth, p.B, paged ? (long long)p.B * p.pt_cols : 0LL);
+            if (!paged_ok)
+                set_error("paged subtree kernel: page-table entries %lld (at most %d), page size %d (at most "
+                          "4096), or K/V cache strides that differ or reach 2^31",
+                          (long long)p.B * p.pt_cols, stream_max_page_entries(), p.page_size);
+            else
+                set_error("no subtree plan fits (b=%d, max_seqlen=%d, max_depth=%d, batch=%d)", p.bdiv.d,
+                          p.max_seqlen, p.max_depth, p.B);
             return QATTN_ERR_ARG;
         }
         if (use) return launch_stream(p, plan, T::kCode, D, pstate, paged, st);

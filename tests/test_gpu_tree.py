@@ -475,6 +475,27 @@ def test_paged_subtree_table_limit():
         ra._paged_forward(Q.to(DEV), Kc, Vc, wide, cu, b, md, None, False, lib.ALGO_SUBTREE)
 
 
+def test_paged_subtree_needs_equal_strides():
+    """The paged subtree kernel addresses K and V with one offset: a V cache
+    with other strides (here every page padded by one slot) runs on the
+    gather kernel under the automatic choice, and is an error when the
+    subtree kernel is forced."""
+    ra, lib = _ra()
+    say("paged strides")
+    lens, b, md = [121] * 3, 3, 4
+    Q, K, V, cu = make_inputs(lens, 4, 64, 2170)
+    Kc, Vc, pt = _shuffled_paged(ra, K, V, cu, 4, 16, 5)
+    big = torch.zeros(Vc.shape[0], 17, *Vc.shape[2:], dtype=Vc.dtype, device=DEV)
+    big[:, :16] = Vc
+    Vs = big[:, :16]  # same values, page stride 17 slots
+    assert Vs.stride() != Kc.stride()
+    o_ref, _, _ = oracle_tree(Q, K, V, cu, b, md)
+    O, _ = ra._paged_forward(Q.to(DEV), Kc, Vs, pt, cu, b, md, None, False, lib.ALGO_AUTO)
+    check_fp16(O.double().cpu().numpy(), o_ref, "paged, V strides differ")
+    with pytest.raises(lib.QAttnError, match="strides"):
+        ra._paged_forward(Q.to(DEV), Kc, Vs, pt, cu, b, md, None, False, lib.ALGO_SUBTREE)
+
+
 def test_paged_missing_pages():
     """Page-table entries that are negative or past num_pages skip the
     ancestors on those pages (qattn.h); a query whose own page and every
