@@ -63,7 +63,7 @@ struct StreamGeom {
     static constexpr int NC = D / 32;                 // 32-element k-chunks of Q K^T
     static constexpr int ND = D / 16;                 // 16-row d-tiles of O^T
     static constexpr size_t LDS_BYTES = ((size_t)(KV_ROWS + Q_ROWS + V_ROWS) * PITCH) * 2 +
-                                        (size_t)Q_ROWS * sizeof(QueryEntry) + kCuCache * 4 + 16 + 128 * 4;
+                                        (size_t)2 * Q_ROWS * sizeof(QueryEntry) + kCuCache * 4 + 16 + 128 * 4;
     // walk export only: the staged row maps (node of each K/V row, token and
     // head offset of each Q row)
     static constexpr size_t DBG_BYTES = (size_t)(KV_ROWS + Q_ROWS) * 4;
@@ -76,7 +76,7 @@ struct StreamGeom {
 // lane i describing BFS level lam_min + i (its first node, node count, LDS row
 // offset = row - node, and first Q row).
 struct TileMeta {
-    int32_t valid, tile, seq, kvh, start, n, lo, hi, lam_min, nlev, rows, nq;
+    int32_t valid, tile, seq, kvh, start, n, lo, lam_min, nlev, rows, nq;
     int64_t kvb;
     int32_t first, cnt, off, qb;
 };
@@ -135,12 +135,12 @@ __device__ __forceinline__ int lane_get(int x, int idx) { return __builtin_amdgc
 // node range), for a sequence spanning tokens [s, e) (cu_seqlens[seq],
 // cu_seqlens[seq + 1], wave-uniform).  Returns true when the level table was
 // (re)computed, false when it was taken from prev (same tile index and
-// sequence length).  band_tb / band_pk: lane i holds plan.tile_base[i] /
-// plan.band[i] (INT32_MAX / 0 past the bands), loaded once per workgroup;
-// lvl_st / lvl_pw: lane l holds plan.lvl_start[l] / plan.lvl_pow[l]; when
-// HAVE_LVL is false they are read here from lvl_lds, the workgroup's LDS copy
-// (a global load in this rarely taken path would make the compiler wait for
-// every load in flight, the next tile's included, before the compute).
+// sequence length).  bpk / tbase: the tile's band (lo | hi << 8 | G << 16)
+// and the band's first tile; lvl_st / lvl_pw: lane l holds plan.lvl_start[l]
+// / plan.lvl_pow[l]; when HAVE_LVL is false they are read here from lvl_lds,
+// the workgroup's LDS copy (a global load in this rarely taken path would
+// make the compiler wait for every load in flight, the next tile's included,
+// before the compute).
 //
 // Every lane works out its own level from the plan's level tables with a few
 // independent operations (the descendants j levels below the root range
@@ -151,14 +151,13 @@ __device__ __forceinline__ int lane_get(int x, int idx) { return __builtin_amdgc
 template <int D, bool HAVE_LVL>
 __device__ __forceinline__ bool tile_setup_se(const TreeParams& p, const SubtreePlan& plan, const StreamArgs& sa,
                                               int w, int32_t s, int32_t e, const TileMeta& prev, TileMeta& t,
-                                              int32_t band_tb, uint32_t band_pk, int32_t lvl_st, uint32_t lvl_pw,
+                                              uint32_t bpk, int tbase, int32_t lvl_st, uint32_t lvl_pw,
                                               const int32_t* lvl_lds) {
     const int lane = threadIdx.x & 63;
     t.valid = 0;
     t.rows = t.nq = 0;
     t.nlev = 0;
     t.lo = 0;
-    t.hi = -1;
     t.lam_min = 0;
     t.start = t.n = 0;
     t.kvb = 0;
@@ -178,7 +177,6 @@ __device__ __forceinline__ bool tile_setup_se(const TreeParams& p, const Subtree
     if (n <= 0) return true;
     if (prev.valid && prev.tile == tile && prev.n == n) {
         t = prev;
-        t.tile = tile;
         t.seq = seq;
         t.kvh = pair - seq * p.Hkv;
         t.start = s;
@@ -190,10 +188,6 @@ __device__ __forceinline__ bool tile_setup_se(const TreeParams& p, const Subtree
         lvl_pw = (uint32_t)lvl_lds[64 + lane];
     }
     const int b = p.bdiv.d;
-    // the tile's band: bands cover ascending tile ranges from tile 0
-    const int bi = (int)__builtin_popcountll(__ballot(tile >= band_tb)) - 1;
-    const uint32_t bpk = (uint32_t)__builtin_amdgcn_readlane((int)band_pk, bi);
-    const int tbase = __builtin_amdgcn_readlane(band_tb, bi);
     int lo = (int)(bpk & 255u), hi = (int)((bpk >> 8) & 255u);
     const int G = (int)(bpk >> 16);
     int64_t r0, r1;  // root range [r0, r1) at level lo
@@ -243,7 +237,6 @@ __device__ __forceinline__ bool tile_setup_se(const TreeParams& p, const Subtree
     t.start = s;
     t.n = n;
     t.lo = lo;
-    t.hi = hi;
     t.lam_min = lam_min;
     t.nlev = nlev;
     t.rows = rows;
@@ -271,7 +264,12 @@ __device__ __forceinline__ bool tile_setup(const TreeParams& p, const SubtreePla
     seq = seq < p.B ? seq : p.B;  // tile_setup_se rejects seq >= B
     const int32_t s = __builtin_amdgcn_readfirstlane(cu_lds[seq]);
     const int32_t e = __builtin_amdgcn_readfirstlane(cu_lds[seq < p.B ? seq + 1 : seq]);
-    return tile_setup_se<D, false>(p, plan, sa, w, s, e, prev, t, band_tb, band_pk, 0, 0u, lvl_lds);
+    // the tile's band: bands cover ascending tile ranges from tile 0
+    const int tile = w - divide(w, sa.tiles_div) * plan.total_tiles;
+    const int bi = (int)__builtin_popcountll(__ballot(tile >= band_tb)) - 1;
+    const uint32_t bpk = (uint32_t)__builtin_amdgcn_readlane((int)band_pk, bi);
+    const int tbase = __builtin_amdgcn_readlane(band_tb, bi);
+    return tile_setup_se<D, false>(p, plan, sa, w, s, e, prev, t, bpk, tbase, 0, 0u, lvl_lds);
 }
 
 // The load rows of a tile (RowMap) from its level table.  Lane x of each
@@ -439,15 +437,16 @@ __device__ __forceinline__ uint2 vt_read4(const uint16_t* Vs, int pitch, int key
     return __builtin_bit_cast(uint2, r);
 }
 
-// Build the query table of a tile: thread q handles query q.  The walk
+// Build the query table of a tile: the calling threads take queries q0,
+// q0 + step, ... (q0 < step, one query per thread and pass).  The walk
 // (src/ragged_attn.py:338-377) attends steps t = 0..min(level, max_depth),
 // levels level - t, exactly the steps with c_t != c_{t-1}; the level loop runs
 // from the deepest level up so every level offset is a wave-uniform readlane.
 __device__ __forceinline__ void build_query_table(const TreeParams& p, const Divider& gdiv, const TileMeta& t,
-                                                  QueryEntry* qt) {
+                                                  QueryEntry* qt, int q0, int step) {
     const int g = p.group;
-    for (int q0 = 0; q0 < t.nq; q0 += kStThreads) {
-        const int q = q0 + (int)threadIdx.x;
+    for (int qs = 0; qs < t.nq; qs += step) {
+        const int q = qs + q0;
         int li = -1, qbl = 0, fi = 0;
         for (int i = 0; i < t.nlev; ++i) {
             const int qi = rl(t.qb, i), ci = rl(t.cnt, i) * g, f = rl(t.first, i);
@@ -749,8 +748,10 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void tree_stream_kernel(
     uint16_t* Ks = smem;
     uint16_t* Qs = Ks + Geo::KV_ROWS * Geo::PITCH;
     uint16_t* Vs = Qs + Geo::Q_ROWS * Geo::PITCH;
+    // two query tables: the compute reads the current tile's while the next
+    // tile's is built (a tile of another shape)
     QueryEntry* qtab = reinterpret_cast<QueryEntry*>(Vs + Geo::V_ROWS * Geo::PITCH);
-    int32_t* cuc = reinterpret_cast<int32_t*>(qtab + Geo::Q_ROWS);
+    int32_t* cuc = reinterpret_cast<int32_t*>(qtab + 2 * Geo::Q_ROWS);
     int32_t* next_slot = cuc + kCuCache;  // the workgroup's next item, written by thread 0
     int32_t* lvl_lds = next_slot + 4;     // plan.lvl_start[0..63], plan.lvl_pow[0..63]
     int32_t* dbg_row = lvl_lds + 128;     // (DBG only: LDS_BYTES + DBG_BYTES are allocated)
@@ -791,7 +792,9 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void tree_stream_kernel(
     const int w = k * sa.ngroups.d + g;
     // the plan's band table, one band per lane, from a single vector load
     // each: the scalar lookup took two dependent kernel-argument round trips
-    // on every workgroup's first tile (~3.8 us at kernel start)
+    // on every workgroup's first tile (~3.8 us at kernel start), and scalar
+    // loads of the first 8 bands (one round trip) finished the first setup
+    // 0.5 us later than these loads
     const int lane = threadIdx.x & 63;
     const int32_t band_tb = lane < kMaxBands ? plan.tile_base[lane] : INT32_MAX;
     const uint32_t band_pk = lane < kMaxBands ? plan.band[lane] : 0u;
@@ -816,7 +819,7 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void tree_stream_kernel(
     // so nothing here waits for vector memory.
     TileMeta cur, none;
     none.valid = 0;
-    int tab_tile = -1, tab_n = -1;  // shape the query table was built for
+    int qcur = 0;  // the query table of the current tile
     RowMap<D> rm;
     Stage<D> sg;
     const int seq0 = tile_seq(sa, w);  // < p.B: w < n_work
@@ -826,7 +829,13 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void tree_stream_kernel(
                                            : p.cu[threadIdx.x];  // p.B < kCuCache = kStThreads
     const int32_t s0 = BATCH ? seq0 * p.max_seqlen : __builtin_amdgcn_readfirstlane(p.cu[seq0]);
     const int32_t e0 = BATCH ? s0 + p.max_seqlen : __builtin_amdgcn_readfirstlane(p.cu[seq0 + 1]);
-    tile_setup_se<D, true>(p, plan, sa, w, s0, e0, none, cur, band_tb, band_pk, lvl_st0, lvl_pw0, lvl_lds);
+    {
+        const int tile0 = w - divide(w, sa.tiles_div) * plan.total_tiles;
+        const int bi = (int)__builtin_popcountll(__ballot(tile0 >= band_tb)) - 1;
+        const uint32_t bpk = (uint32_t)__builtin_amdgcn_readlane((int)band_pk, bi);
+        const int tbase = __builtin_amdgcn_readlane(band_tb, bi);
+        tile_setup_se<D, true>(p, plan, sa, w, s0, e0, none, cur, bpk, tbase, lvl_st0, lvl_pw0, lvl_lds);
+    }
     // the level tables for later tiles' setups (published by the first loop top's barrier)
     if (threadIdx.x < 64) {
         lvl_lds[threadIdx.x] = lvl_st0;
@@ -838,9 +847,7 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void tree_stream_kernel(
         tile_issue<D, BATCH, PAGED>(p, cur, rm, sg, pt_lds, rowok);
         // the first query table is built while the first loads are in flight
         // (the first loop top's barrier publishes it)
-        build_query_table(p, gdiv, cur, qtab);
-        tab_tile = cur.tile;
-        tab_n = cur.n;
+        build_query_table(p, gdiv, cur, qtab, threadIdx.x, kStThreads);
     }
     if (dyn && leader) ans = sched_grab(grab_ctr);  // answered by the first loop top
     bool first = true;
@@ -860,34 +867,39 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void tree_stream_kernel(
         const bool more = kn < sa.items;
         const int wn = kn * sa.ngroups.d + g;
         TileMeta nxt;
+        int qnxt = qcur;
+        bool build = false;
         if (more) {
             const bool fresh = tile_setup<D>(p, plan, sa, cu_lds, wn, cur, nxt, band_tb, band_pk, lvl_lds);
             if (nxt.valid) {
                 if (fresh) tile_rowmap<D, PAGED>(p, gdiv, nxt, rm);
                 tile_issue<D, BATCH, PAGED>(p, nxt, rm, sg, pt_lds, rowok + (par ^ 1) * Geo::KV_ROWS);
+                // the next tile's query table: the current one, or (another
+                // shape) built into the other one after this compute
+                build = !cur.valid || nxt.tile != cur.tile || nxt.n != cur.n;
+                qnxt = build ? qcur ^ 1 : qcur;
             }
         }
         // the next item, or (after this workgroup's last request) done
         if (dyn && leader) ans = sched_grab(more ? grab_ctr : done_ctr);
         if (cur.valid) {
-            // the query table follows the tile shape (uniform branch)
-            if (cur.tile != tab_tile || cur.n != tab_n) {
-                build_query_table(p, gdiv, cur, qtab);
-                tab_tile = cur.tile;
-                tab_n = cur.n;
-                __syncthreads();
-            }
+            const QueryEntry* qt = qtab + qcur * Geo::Q_ROWS;
             // the rows that exist: all, or (paged) those whose page does
             uint64_t vmask = ~uint64_t(0);
             if constexpr (PAGED) vmask = __ballot(lane < Geo::KV_ROWS && rowok[par * Geo::KV_ROWS + lane] != 0);
-            if constexpr (DBG) dbg_walk_export(p, cur, qtab, dbg_row, dbg_q, vmask);
-            tile_compute<T, D, LSE, PSTATE, BATCH>(p, cur, Ks, Vs, Qs, qtab, vmask);
+            if constexpr (DBG) dbg_walk_export(p, cur, qt, dbg_row, dbg_q, vmask);
+            tile_compute<T, D, LSE, PSTATE, BATCH>(p, cur, Ks, Vs, Qs, qt, vmask);
         }
+        // by the last wave, which computes the fewest query blocks (the
+        // barrier below publishes it)
+        if (build && threadIdx.x >= kStThreads - 64)
+            build_query_table(p, gdiv, nxt, qtab + qnxt * Geo::Q_ROWS, lane, 64);
         __syncthreads();
         if (!more) break;
         cur = nxt;
         k = kn;
         par ^= 1;
+        qcur = qnxt;
     }
     // The last workgroup of the group to finish clears its counters: every
     // other one has made its last request before adding to done_ctr.

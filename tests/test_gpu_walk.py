@@ -76,6 +76,12 @@ HEAP_CASES = [
     ([4681], 8, 4, 4, 4, 64),             # cfg5's tree
     ([3000, 511], 2, 11, 4, 1, 128),      # deep binary, ragged, GQA 4
     ([100], 7, 0, 4, 4, 32),              # max_depth 0: self only
+    # enough tiles that the subtree kernel runs its last round as half tiles
+    # (halves of root ranges, of one root's children, of chain levels)
+    ([2000] * 8, 1, 8, 16, 16, 128),      # b=1 chains
+    ([1365, 700] * 4, 4, 2, 32, 32, 128), # ragged + truncated
+    ([4681] * 4, 8, 4, 32, 8, 64),        # cfg5's tree, GQA 4
+    ([1093, 50, 0, 1093], 3, 6, 32, 16, 32),  # b=3, ragged + empty, GQA 2
 ]
 
 
