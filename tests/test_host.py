@@ -165,6 +165,28 @@ def test_abi_prefix_only_validation():
     assert L.qattn_prefix_workspace_bytes(1, 15, 15, 4, 4, 64, 512, 2) == 2 * a256(2 * 60 * 4) + a256(2 * 60 * 64 * 4)
 
 
+def test_abi_prefix_split_rule():
+    """The automatic prefix split count, read back through the workspace size
+    (one (m, l, acc) state per split; a single split fuses the walk and needs
+    none): enough (sequence, kv head, 128-row tile) units for ~512 workgroups,
+    at least an eighth of the 64-key blocks (2..8) per split."""
+    L = _lib.lib()
+    a256 = lambda x: (x + 255) // 256 * 256
+
+    def ws(splits, T, Hq, D):
+        return 0 if splits <= 1 else 2 * a256(splits * T * Hq * 4) + a256(splits * T * Hq * D * 4)
+
+    # one EAGLE-3 step: 16 units, 32 blocks -> 8 splits of 4 blocks
+    assert L.qattn_prefix_workspace_bytes(1, 60, 60, 32, 8, 128, 2048, 0) == ws(8, 60, 32, 128)
+    # cfg4: 96 units -> 5 splits (of 32 blocks)
+    assert L.qattn_prefix_workspace_bytes(4, 85, 340, 32, 8, 128, 10240, 0) == ws(5, 340, 32, 128)
+    # cfg5: 18944 units fill the GPU -> one split
+    assert L.qattn_prefix_workspace_bytes(16, 4681, 16 * 4681, 32, 32, 128, 2048, 0) == 0
+    # a 2-block prefix stays whole; a 16-block one splits into 8 of 2
+    assert L.qattn_prefix_workspace_bytes(1, 60, 60, 32, 8, 128, 128, 0) == 0
+    assert L.qattn_prefix_workspace_bytes(1, 60, 60, 32, 8, 128, 1024, 0) == ws(8, 60, 32, 128)
+
+
 def test_abi_ragged_tree_attn_validation():
     """qattn_ragged_tree_attn_fwd over [B, H, N, D] strides: every layout it
     cannot address is rejected before any launch; a valid layout with L = 512
