@@ -1,6 +1,7 @@
 """Benchmark of the tree-verify attention hot path on one MI355X.
 
-    python bench.py [--steps K] [--warmup W] [--config cfg2|cfg3|cfg4|cfg4_prefix|cfg5|gen1024|cfg4_bhnd|cfg2_paged|eagle3|merge4]
+    python bench.py [--steps K] [--warmup W] [--config cfg2|cfg3|cfg4|cfg4_prefix|cfg5|gen1024|cfg4_bhnd|cfg2_paged|eagle3|merge4
+                    |cfg2_bf16|cfg4_bf16]
                     [--algo auto|gather|subtree] [--no-extra] [--no-cpu-baseline]
 
 A step is one full verify-attention call (all sequences, all heads, and the
@@ -80,7 +81,17 @@ CONFIGS = {
     # cfg4's prefix pass alone (prefix_attention: the same queries and prefix,
     # no tree keys), the denominator of the cfg4 verify/prefix-only ratio
     "cfg4_prefix": dict(B=4, b=4, d=3, H=32, Hkv=8, D=128, L=10240, sigma=1.0, layout="prefix_only"),
+    # cfg2 and cfg4 in bfloat16 (the reference takes fp16 or bf16,
+    # src/ragged_attn.py:1113-1116)
+    "cfg2_bf16": dict(B=4, b=4, d=5, H=32, Hkv=32, D=128, L=0, sigma=1.0, dtype="bf16"),
+    "cfg4_bf16": dict(B=4, b=4, d=3, H=32, Hkv=8, D=128, L=10240, sigma=1.0, dtype="bf16"),
 }
+
+
+def torch_dtype(c):
+    """The config's element type (fp16 unless it names bf16)."""
+    import torch
+    return torch.bfloat16 if c.get("dtype") == "bf16" else torch.float16
 
 
 def num_tree_nodes(b, d):
@@ -196,7 +207,7 @@ def cpu_baseline(c, budget_s=20.0):
     torch.set_num_threads(cores)
     B, b, d = c["B"], c["b"], c["d"]
     N = tree_size(c)
-    Q, K, V, Kp, Vp = make_set(c, B * 10000 + b * 100 + d, torch.float16)
+    Q, K, V, Kp, Vp = make_set(c, B * 10000 + b * 100 + d, torch_dtype(c))
     nseq = B
     if c["L"] and B * N * (N + c["L"]) * c["H"] > 4e9:
         nseq = 1  # sample: one sequence of the batch (the full score tensor would not fit)
@@ -351,7 +362,7 @@ def build_workload(name, algo, forced_sets=0):
     layout = c.get("layout")
     sets = []
     for i in range(nsets):
-        Q, K, V, Kp, Vp = make_set(c, seed + i, torch.float16)
+        Q, K, V, Kp, Vp = make_set(c, seed + i, torch_dtype(c))
         if layout == "bhnd":
             # the same values in the E2E layout: prefix rows then tree rows per sequence
             Q = Q.view(B, N, H, D).permute(0, 2, 1, 3).contiguous()
@@ -523,11 +534,11 @@ def main():
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f16",
+        "dtype": c.get("dtype", "f16"),
         "data": (f"synthetic N(0,{c['sigma']}^2), CPU-seeded (seed B*10000+b*100+d + set), {nsets} input sets "
                  "rotated call by call"),
         "config": {"workload": f"{args.config}: verify attention B={B} b={b} d={d} N={N} H={H} Hkv={Hkv} "
-                               f"D={D} L={L} fp16" + (", explicit parents" if parents_walk else "")
+                               f"D={D} L={L} {c.get('dtype', 'fp16')}" + (", explicit parents" if parents_walk else "")
                                + (", [B, H, N, D] views" if layout == "bhnd" else "")
                                + (", paged K/V (16-token pages, shuffled)" if layout == "paged" else "")
                                + (", fused_lse_merge of two [B, H, Nq, D] blocks" if layout == "merge" else "")

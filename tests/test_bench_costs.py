@@ -73,6 +73,9 @@ def test_prefix_configs():
     # the same workload in other layouts costs the same
     assert bench.model_costs(bench.CONFIGS["cfg4_bhnd"]) == bench.model_costs(bench.CONFIGS["cfg4"])
     assert bench.model_costs(bench.CONFIGS["cfg2_paged"]) == bench.model_costs(bench.CONFIGS["cfg2"])
+    # bf16 moves the same number of 2-byte elements
+    assert bench.model_costs(bench.CONFIGS["cfg2_bf16"]) == bench.model_costs(bench.CONFIGS["cfg2"])
+    assert bench.model_costs(bench.CONFIGS["cfg4_bf16"]) == bench.model_costs(bench.CONFIGS["cfg4"])
 
 
 def test_more_than_one_gpu_is_refused():
