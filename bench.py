@@ -196,7 +196,7 @@ def copy_calibration(mib):
     print(json.dumps({"copy_calibration_bytes": n, "copies": 3}), flush=True)
 
 
-def cpu_baseline(c, budget_s=20.0):
+def cpu_baseline(c, budget_s=12.0):
     """Reference CPU path on a bounded sample: padded SDPA (fp32, MATH) with
     the tree mask (prefix columns all-attend), repeated until ~budget_s."""
     import numpy as np
@@ -232,7 +232,7 @@ def cpu_baseline(c, budget_s=20.0):
     t0 = time.perf_counter()
     run()  # warmup
     first = time.perf_counter() - t0
-    iters = max(1, min(20, int(budget_s / max(first, 1e-3))))
+    iters = max(3, min(60, int(budget_s / max(first, 1e-3))))
     times = []
     for _ in range(iters):
         t0 = time.perf_counter()

@@ -43,7 +43,7 @@ struct PrefixParams {
     const int32_t* cu;
     float* part_m;
     float* part_l;
-    float* part_acc;
+    void* part_acc;  // numerator / l: fp16 for fp16 inputs, else fp32 (kPartHalf)
     int64_t sq_t, sq_h;
     int64_t skp_b, skp_t, skp_h, svp_b, svp_t, svp_h;
     int64_t total_tokens;
@@ -422,7 +422,11 @@ __global__ __launch_bounds__(kPrefixThreads) __attribute__((amdgpu_waves_per_eu(
     }
 
     if constexpr (!FUSED) {
-        // ---- partial state of this split: (m, l, unnormalised acc) ----
+        // ---- partial state of this split: (m, l, acc / l).  For fp16
+        // inputs the normalised numerator is stored in fp16, which halves the
+        // bytes the merge reads, as the reference's own split pipelines hand
+        // fp16 partial outputs to their merge (scripts/benchmark_micro.py:
+        // 576-592, src/ragged_attn.py:1619); bf16 inputs keep fp32 states. ----
         const int64_t plane = p.total_tokens * (int64_t)p.Hq;
 #pragma unroll
         for (int b = 0; b < kQB; ++b) {
@@ -434,11 +438,19 @@ __global__ __launch_bounds__(kPrefixThreads) __attribute__((amdgpu_waves_per_eu(
                 p.part_m[idx] = m_run[b];
                 p.part_l[idx] = l_tot[b];
             }
-            float* dst = p.part_acc + idx * D + 4 * lq;
+            const float inv = l_tot[b] > 0.f ? 1.f / l_tot[b] : 0.f;
+            const int64_t off = idx * D + 4 * lq;
 #pragma unroll
-            for (int dt = 0; dt < ND; ++dt)
-                *reinterpret_cast<float4*>(dst + 16 * dt) =
-                    make_float4(oacc[b][dt][0], oacc[b][dt][1], oacc[b][dt][2], oacc[b][dt][3]);
+            for (int dt = 0; dt < ND; ++dt) {
+                if constexpr (kPartHalf<T>)
+                    *reinterpret_cast<uint2*>((uint16_t*)p.part_acc + off + 16 * dt) =
+                        make_uint2(MfmaOps<F16>::pack2(oacc[b][dt][0] * inv, oacc[b][dt][1] * inv),
+                                   MfmaOps<F16>::pack2(oacc[b][dt][2] * inv, oacc[b][dt][3] * inv));
+                else
+                    *reinterpret_cast<float4*>((float*)p.part_acc + off + 16 * dt) =
+                        make_float4(oacc[b][dt][0] * inv, oacc[b][dt][1] * inv, oacc[b][dt][2] * inv,
+                                    oacc[b][dt][3] * inv);
+            }
         }
     } else {
         // ---- fused epilogue: each wave re-lays both of its 16-row blocks in
@@ -647,7 +659,7 @@ __global__ __launch_bounds__(kPrefixThreads) void prefix_merge_kernel(TreeParams
     if (tok >= n) return;
     const int64_t qrow = (int64_t)start + tok;
     float m, l, acc[8 * (D / 32)];
-    load_partial_state4<D>(p, qrow, h, j, m, l, acc);
+    load_partial_state4<T, D>(p, qrow, h, j, m, l, acc);
     write_out4<T, D, LSE, BATCH>(p, seq, qrow, h, j, m, l, acc);
 }
 
@@ -714,6 +726,7 @@ static int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
 static int64_t workspace_bytes(int64_t total_tokens, int hq, int head_dim, int splits) {
     if (splits <= 1) return 0;  // one split: fused epilogue, no partial states
     const int64_t plane = total_tokens * hq;
+    // (m, l and the numerator in fp32: the bf16 layout; fp16 uses half of the last)
     return 2 * align256(splits * plane * 4) + align256(splits * plane * head_dim * 4);
 }
 
@@ -874,7 +887,7 @@ static int prefix_tree_impl(const void* q, const int64_t q_stride[3], const void
     if (!fused) {
         pp.part_m = (float*)workspace;
         pp.part_l = (float*)((char*)workspace + align256(splits * plane * 4));
-        pp.part_acc = (float*)((char*)workspace + 2 * align256(splits * plane * 4));
+        pp.part_acc = (char*)workspace + 2 * align256(splits * plane * 4);
     }
     pp.sq_t = q_stride[0];
     pp.sq_h = q_stride[1];

@@ -73,7 +73,7 @@ struct TreeParams {
     // split-K prefix partial state merged into the tree state (may be null)
     const float* part_m;        // [n_split][T][Hq]   running max (log2 domain)
     const float* part_l;        // [n_split][T][Hq]   running denominator
-    const float* part_acc;      // [n_split][T][Hq][D] unnormalised numerator
+    const void* part_acc;       // [n_split][T][Hq][D] numerator / l: fp16 for fp16 inputs, else fp32
     int32_t n_split;
     // tree K/V location of sequence `seq` is cu[seq] + kv_seq_off * seq
     // (0 for the packed layout; the hybrid layout places L prefix rows before

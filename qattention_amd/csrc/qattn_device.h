@@ -188,6 +188,14 @@ struct MfmaOps<BF16> {
     static __device__ __forceinline__ float hi(uint32_t w) { return __builtin_bit_cast(float, w & 0xffff0000u); }
 };
 
+// Prefix split states store each query's numerator / l, a convex
+// combination of V rows: in fp16 for fp16 inputs (it fits fp16's range, and
+// half the bytes of fp32 is half of what the split merge reads), in fp32 for
+// bf16 inputs (bf16's 8-bit mantissa would add a second rounding the size of
+// the output's own).
+template <typename T>
+constexpr bool kPartHalf = T::kCode == F16::kCode;
+
 __device__ __forceinline__ float xor_max(float x, int m) { return fmaxf(x, __shfl_xor(x, m)); }
 
 // Reductions over the 4 lanes l, l^16, l^32, l^48 (one MFMA output column)

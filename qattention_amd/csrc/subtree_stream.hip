@@ -601,16 +601,24 @@ __device__ __forceinline__ void block_compute(const TreeParams& p, const TileMet
                 for (int s = 0; s < p.n_split; ++s) {
                     const float ms = p.part_m[s * plane + idx];
                     if (ms == -INFINITY) continue;
-                    const float w = fast_exp2(ms - mref);
-                    lpre = __builtin_fmaf(w, p.part_l[s * plane + idx], lpre);
-                    const float* a = p.part_acc + (s * plane + idx) * D + 4 * i4;
+                    // the split's numerator is stored as acc / l (kPartHalf)
+                    const float wl = fast_exp2(ms - mref) * p.part_l[s * plane + idx];
+                    lpre += wl;
+                    const int64_t off = (s * plane + idx) * D + 4 * i4;
 #pragma unroll
                     for (int dt = 0; dt < ND; ++dt) {
-                        const float4 v = *reinterpret_cast<const float4*>(a + 16 * dt);
-                        oacc[dt][0] = __builtin_fmaf(w, v.x, oacc[dt][0]);
-                        oacc[dt][1] = __builtin_fmaf(w, v.y, oacc[dt][1]);
-                        oacc[dt][2] = __builtin_fmaf(w, v.z, oacc[dt][2]);
-                        oacc[dt][3] = __builtin_fmaf(w, v.w, oacc[dt][3]);
+                        float4 v;
+                        if constexpr (kPartHalf<T>) {
+                            const uint2 h = *reinterpret_cast<const uint2*>((const uint16_t*)p.part_acc + off + 16 * dt);
+                            v = make_float4(MfmaOps<F16>::lo(h.x), MfmaOps<F16>::hi(h.x), MfmaOps<F16>::lo(h.y),
+                                            MfmaOps<F16>::hi(h.y));
+                        } else {
+                            v = *reinterpret_cast<const float4*>((const float*)p.part_acc + off + 16 * dt);
+                        }
+                        oacc[dt][0] = __builtin_fmaf(wl, v.x, oacc[dt][0]);
+                        oacc[dt][1] = __builtin_fmaf(wl, v.y, oacc[dt][1]);
+                        oacc[dt][2] = __builtin_fmaf(wl, v.z, oacc[dt][2]);
+                        oacc[dt][3] = __builtin_fmaf(wl, v.w, oacc[dt][3]);
                     }
                 }
             }

@@ -90,7 +90,7 @@ __global__ __launch_bounds__(kThreads) void tree_gather_kernel(TreeParams p) {
                                                           LAYOUT == KV_PAGED ? qdummy : nullptr, dbg);
     w.issue();
     if constexpr (PSTATE) {
-        load_partial_state4<D>(p, qrow, h, j, m, l, acc);
+        load_partial_state4<T, D>(p, qrow, h, j, m, l, acc);
     } else {
 #pragma unroll
         for (int e = 0; e < 8 * NCH; ++e) acc[e] = 0.f;

@@ -74,15 +74,19 @@ __device__ __forceinline__ void load_q4(const TreeParams& p, int seq, int64_t qr
 }
 
 // Initial state from split-K prefix partials (flash-decoding merge of all
-// splits): m = max_s m_s, l = sum_s 2^(m_s - m) l_s, acc likewise.  The splits
+// splits): m = max_s m_s, w_s = 2^(m_s - m) l_s, l = sum_s w_s and acc =
+// sum_s w_s a_s, a_s being split s's numerator / l_s as stored (fp16 for
+// fp16 inputs, else fp32: see kPartHalf).  The splits
 // are folded in batches of SP whose loads are issued together, each batch
 // moving the running maximum once (an online merge: no separate pass for the
 // maxima), so n splits cost about n / SP memory round trips.
-template <int D>
+template <typename T, int D>
 __device__ __forceinline__ void load_partial_state4(const TreeParams& p, int64_t qrow, int h, int j,
                                                     float& m, float& l, float* acc) {
     constexpr int NCH = D / 32;
     constexpr int SP = 12 / NCH;  // splits per batch: 3 at head_dim 128
+    constexpr bool H = kPartHalf<T>;
+    constexpr int W = H ? 1 : 2;  // 16-byte loads per 8-element chunk
     const int ns = p.n_split;
     const int64_t plane = p.total_tokens * (int64_t)p.Hq;
     const int64_t idx = qrow * p.Hq + h;
@@ -92,22 +96,26 @@ __device__ __forceinline__ void load_partial_state4(const TreeParams& p, int64_t
     for (int e = 0; e < 8 * NCH; ++e) acc[e] = 0.f;
     for (int s0 = 0; s0 < ns; s0 += SP) {
         float ms[SP], ls[SP];
-        float4 a[SP][2 * NCH];
+        Vec16 a[SP][W * NCH];  // numerator / l of split s0 + u, 8 elements per chunk
 #pragma unroll
         for (int u = 0; u < SP; ++u) {
             ms[u] = -INFINITY;
             ls[u] = 0.f;
 #pragma unroll
-            for (int i = 0; i < 2 * NCH; ++i) a[u][i] = make_float4(0.f, 0.f, 0.f, 0.f);
+            for (int i = 0; i < W * NCH; ++i) a[u][i] = Vec16{{0u, 0u, 0u, 0u}};
             if (s0 + u < ns) {  // wave-uniform
                 const int64_t k = (s0 + u) * plane + idx;
                 ms[u] = p.part_m[k];
                 ls[u] = p.part_l[k];
-                const float* src = p.part_acc + k * D + 8 * j;
 #pragma unroll
                 for (int i = 0; i < NCH; ++i) {
-                    a[u][2 * i] = *reinterpret_cast<const float4*>(src + 32 * i);
-                    a[u][2 * i + 1] = *reinterpret_cast<const float4*>(src + 32 * i + 4);
+                    if constexpr (H) {
+                        a[u][i] = ld16((const uint16_t*)p.part_acc + k * D + 8 * j + 32 * i);
+                    } else {
+                        const float* src = (const float*)p.part_acc + k * D + 8 * j + 32 * i;
+                        a[u][2 * i] = ld16(src);
+                        a[u][2 * i + 1] = ld16(src + 4);
+                    }
                 }
             }
         }
@@ -125,19 +133,18 @@ __device__ __forceinline__ void load_partial_state4(const TreeParams& p, int64_t
 #pragma unroll
         for (int u = 0; u < SP; ++u) {
             const float w = ms[u] == -INFINITY ? 0.f : fast_exp2(ms[u] - m);
-            l = __builtin_fmaf(w, ls[u], l);
+            const float wl = w * ls[u];  // weight of the normalised numerator
+            l += wl;
 #pragma unroll
             for (int i = 0; i < NCH; ++i) {
-                const float4 a0 = a[u][2 * i], a1 = a[u][2 * i + 1];
                 float* c = acc + 8 * i;
-                c[0] = __builtin_fmaf(w, a0.x, c[0]);
-                c[1] = __builtin_fmaf(w, a0.y, c[1]);
-                c[2] = __builtin_fmaf(w, a0.z, c[2]);
-                c[3] = __builtin_fmaf(w, a0.w, c[3]);
-                c[4] = __builtin_fmaf(w, a1.x, c[4]);
-                c[5] = __builtin_fmaf(w, a1.y, c[5]);
-                c[6] = __builtin_fmaf(w, a1.z, c[6]);
-                c[7] = __builtin_fmaf(w, a1.w, c[7]);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float x = H ? ((e & 1) ? MfmaOps<F16>::hi(a[u][i].w[e >> 1])
+                                                 : MfmaOps<F16>::lo(a[u][i].w[e >> 1]))
+                                      : __builtin_bit_cast(float, a[u][2 * i + (e >> 2)].w[e & 3]);
+                    c[e] = __builtin_fmaf(wl, x, c[e]);
+                }
             }
         }
     }

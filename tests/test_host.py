@@ -160,7 +160,9 @@ def test_abi_prefix_only_validation():
     assert call(kps=(512 * 256, 252, 64)) == -4
     assert call() == -5
     assert call(batch=0) == 0
-    # two splits of (m, l, acc) over 15 tokens x 4 heads, each array 256-byte aligned
+    # two splits of (m, l, numerator / l) over 15 tokens x 4 heads, sized for
+    # fp32 states (bf16 inputs; fp16 ones store the numerator in half of it),
+    # each array 256-byte aligned
     a256 = lambda x: (x + 255) // 256 * 256
     assert L.qattn_prefix_workspace_bytes(1, 15, 15, 4, 4, 64, 512, 2) == 2 * a256(2 * 60 * 4) + a256(2 * 60 * 64 * 4)
 
