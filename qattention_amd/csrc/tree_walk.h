@@ -84,9 +84,11 @@ template <typename T, int D>
 __device__ __forceinline__ void load_partial_state4(const TreeParams& p, int64_t qrow, int h, int j,
                                                     float& m, float& l, float* acc) {
     constexpr int NCH = D / 32;
-    constexpr int SP = 12 / NCH;  // splits per batch: 3 at head_dim 128
     constexpr bool H = kPartHalf<T>;
     constexpr int W = H ? 1 : 2;  // 16-byte loads per 8-element chunk
+    // splits per batch: 4 (fp16 states) or 3 (fp32) at head_dim 128; 6 fp16
+    // states per batch needed more than 256 VGPRs in the gather kernel
+    constexpr int SP = (H && NCH == 4) ? 4 : 12 / NCH;
     const int ns = p.n_split;
     const int64_t plane = p.total_tokens * (int64_t)p.Hq;
     const int64_t idx = qrow * p.Hq + h;
