@@ -52,11 +52,11 @@ PEAK_MFMA = 2.5e15    # FLOP/s, MI355X dense fp16 MFMA (vendor figure)
 CALLS_PER_GRAPH = 32  # a graph launch leaves ~8 µs between graphs; 32 calls amortise it
 SETTLE_S = 0.1        # untimed replays before the warmup steps (clock settling)
 
-# BASELINE.json configs[1..4], and the explicit-parents workload of the
-# reference's model-generality benchmark (scripts/benchmark_model_generality.py:
-# 19-53: B=1, heap parents (i-1)//b with the root its own parent, b=10 d=7
-# capped at N=1024 nodes, Llama-3.1-8B heads; BASELINE.md quotes 113.0 µs on
-# unrecorded hardware)
+# The reference's configs cfg2..cfg5, and the explicit-parents workload of its
+# model-generality benchmark (scripts/benchmark_model_generality.py:19-53:
+# B=1, heap parents (i-1)//b with the root its own parent, b=10 d=7 capped at
+# N=1024 nodes, Llama-3.1-8B heads; results/generality/
+# model_generality_benchmark.csv:6 records 113.0 µs on unrecorded hardware)
 CONFIGS = {
     "cfg2": dict(B=4, b=4, d=5, H=32, Hkv=32, D=128, L=0, sigma=1.0),
     "cfg3": dict(B=8, b=2, d=9, H=32, Hkv=32, D=128, L=0, sigma=1.0),

@@ -207,7 +207,7 @@ def test_prefix_equals_merge_pipeline():
 
 
 # ---------------------------------------------------------------------------
-# full-size BASELINE prefix configurations
+# full-size prefix configurations of the reference benchmark (cfg4, cfg5)
 # ---------------------------------------------------------------------------
 
 def test_cfg4_full_size():

@@ -192,8 +192,9 @@ def test_golden_fixture(path):
 
 
 def test_golden_cfg1_fp16():
-    """BASELINE configs[0] fixture (fp32 inputs) through the fp16 kernel: the
-    kernel output matches the oracle evaluated on the fp16-rounded inputs."""
+    """cfg1 fixture (the reference's CPU-runnable configuration, fp32 inputs)
+    through the fp16 kernel: the kernel output matches the oracle evaluated on
+    the fp16-rounded inputs."""
     z = np.load(os.path.join(GOLDEN_DIR, "cfg1.npz"))
     Q, K, V = (torch.from_numpy(z[n]).half() for n in ("q", "k", "v"))
     cu = torch.from_numpy(z["cu"])
@@ -594,7 +595,7 @@ def test_fused_lse_merge(dtype):
 
 
 # ---------------------------------------------------------------------------
-# full-size BASELINE configurations (tree-only)
+# full-size tree-only configurations of the reference benchmark (cfg2, cfg3)
 # ---------------------------------------------------------------------------
 
 @pytest.mark.parametrize("B,b,d", [(4, 4, 5), (8, 2, 9)])

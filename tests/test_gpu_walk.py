@@ -62,7 +62,7 @@ def _tree_call(Q, K, V, cu, b, md, algo, table, max_seqlen=None):
     return O
 
 
-# (lens, b, max_depth, Hq, Hkv, D): BASELINE cfg2 / cfg3 at full size, a
+# (lens, b, max_depth, Hq, Hkv, D): cfg2 / cfg3 at full size, a
 # many-band plan (b=4 d=7, N=21845), truncated walks, b=1 chains, ragged and
 # empty sequences, GQA, every head dim
 HEAP_CASES = [
