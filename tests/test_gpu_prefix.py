@@ -151,6 +151,35 @@ def test_prefix_split_counts_agree():
         check_fp16(O.double().cpu().numpy(), o_ref, f"splits={ns}")
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_prefix_split_states_large_values(dtype):
+    """Split states store numerator / l (fp16 for fp16 inputs, fp32 for bf16):
+    with V values up to ~3e4 every split count stays within the output's own
+    relative rounding bound of the fp64 oracle (O is a convex combination of V
+    rows, so no state leaves the input range)."""
+    ra = _ra()
+    Q, K, V, cu = make_inputs([85, 40], 8, 128, 911, dtype=dtype, Hkv=2)
+    Kp, Vp = _prefix(2, 1500, 2, 128, 912, dtype=dtype)
+    V = (V.float() * 8192).to(dtype)
+    Vp = (Vp.float() * 8192).to(dtype)
+    assert float(V.float().abs().max()) < 6e4 and float(Vp.float().abs().max()) < 6e4
+    o_ref, lse_ref, _ = oracle_tree(Q, K, V, cu, 4, 3, Kp=Kp, Vp=Vp)
+    args = (Q.to(DEV), K.to(DEV), V.to(DEV), cu, Kp.to(DEV), Vp.to(DEV), 4, 3)
+    for ns in (1, 3, 8, 0):
+        say("large values, splits", ns, dtype)
+        O, LSE = ra.ragged_attention_prefix(*args, num_splits=ns, return_lse=True)
+        o = O.double().cpu().numpy()
+        assert np.isfinite(o).all(), f"splits={ns}"
+        # the unit-scale bounds of check_fp16 / check_bf16 scaled by V's 2^13
+        if dtype == torch.float16:
+            bound = 2e-3 * np.maximum(8192.0, np.abs(o_ref))
+        else:
+            bound = 2.0 ** -7 * np.maximum(8192.0, np.abs(o_ref)) + 8192 * 1e-3
+        err = np.abs(o - o_ref)
+        assert (err <= bound).all(), f"splits={ns}: max err {err.max():.3e}"
+        assert np.abs(LSE.double().cpu().numpy() - lse_ref).max() <= (1e-4 if dtype == torch.float16 else 2e-3)
+
+
 def test_prefix_shared_and_strided():
     """A prefix shared by the batch ([L, Hkv, D]) and a permuted view of a
     [B, Hkv, L, D] cache (the HF layout)."""
