@@ -1,7 +1,7 @@
 """Benchmark of the tree-verify attention hot path on one MI355X.
 
     python bench.py [--steps K] [--warmup W] [--config cfg2|cfg3|cfg4|cfg4_prefix|cfg5|gen1024|cfg4_bhnd|cfg2_paged|eagle3|merge4
-                    |cfg2_bf16|cfg4_bf16]
+                    |cfg2_bf16|cfg4_bf16|cfg4_shared]
                     [--algo auto|gather|subtree] [--no-extra] [--no-cpu-baseline]
 
 A step is one full verify-attention call (all sequences, all heads, and the
@@ -85,6 +85,10 @@ CONFIGS = {
     # src/ragged_attn.py:1113-1116)
     "cfg2_bf16": dict(B=4, b=4, d=5, H=32, Hkv=32, D=128, L=0, sigma=1.0, dtype="bf16"),
     "cfg4_bf16": dict(B=4, b=4, d=3, H=32, Hkv=8, D=128, L=10240, sigma=1.0, dtype="bf16"),
+    # cfg4 with one prefix shared by the batch ([L, Hkv, D], the first
+    # sequence's prefix for all four), as the reference's micro-benchmark
+    # shares K_sh/V_sh across its branches (scripts/benchmark_micro.py:318-331)
+    "cfg4_shared": dict(B=4, b=4, d=3, H=32, Hkv=8, D=128, L=10240, sigma=1.0, layout="shared_prefix"),
 }
 
 
@@ -154,6 +158,8 @@ def model_costs(c):
         return 3 * 2 * T * H * D + 2 * 4 * T * H, 6 * T * H * D, 0
     tree_bytes = 2 * T * D * (2 * H + 2 * Hkv)          # Q + O at H, tree K + V at Hkv
     prefix_bytes = 2 * 2 * B * L * Hkv * D                 # prefix K + V at Hkv
+    if c.get("layout") == "shared_prefix":
+        prefix_bytes //= B                                 # one prefix for the batch
     prefix_flops = 4 * B * N * H * L * D
     if c.get("layout") == "prefix_only":
         return 2 * T * D * 2 * H + prefix_bytes, prefix_flops, prefix_flops
@@ -212,6 +218,8 @@ def cpu_baseline(c, budget_s=12.0):
     if c["L"] and B * N * (N + c["L"]) * c["H"] > 4e9:
         nseq = 1  # sample: one sequence of the batch (the full score tensor would not fit)
     Q, K, V = (t[:nseq * N].float() for t in (Q, K, V))
+    if c.get("layout") == "shared_prefix":  # the first sequence's prefix for every sequence
+        Kp, Vp = (t[:1].expand(nseq, -1, -1, -1) for t in (Kp, Vp))
     Kp = Kp[:nseq].float() if Kp is not None else None
     Vp = Vp[:nseq].float() if Vp is not None else None
     cu = torch.arange(0, (nseq + 1) * N, N, dtype=torch.int32)
@@ -384,6 +392,8 @@ def build_workload(name, algo, forced_sets=0):
             Vp = torch.randn(B, H, N, generator=g) * 3
         if layout == "prefix_only":
             K = V = None  # no tree keys
+        if layout == "shared_prefix":
+            Kp, Vp = Kp[0], Vp[0]  # [L, Hkv, D]: sequence stride 0
         sets.append([t.to(dev) if t is not None else None for t in (Q, K, V, Kp, Vp)])
     cu = torch.arange(0, (B + 1) * N, N, dtype=torch.int32, device=dev)
     parents = torch.tensor(tree_parents(c) * B, dtype=torch.int32, device=dev) if parents_walk else None

@@ -114,3 +114,9 @@ def test_rotation_defeats_the_infinity_cache(name):
         assert all(m <= bench.CALLS_PER_GRAPH for _, m in chunks)
         sets = [k % n for k in calls]
         assert all(a != b for a, b in zip(sets, sets[1:]))
+    # a prefix shared by the batch is read once: cfg4's bytes less 3 of its 4
+    # prefixes (K + V, 10240 x 8 x 128 fp16 each), the same FLOPs
+    b4, f4, p4 = bench.model_costs(bench.CONFIGS["cfg4"])
+    bs, fs, ps = bench.model_costs(bench.CONFIGS["cfg4_shared"])
+    assert (bs, fs, ps) == (b4 - 3 * 2 * 2 * 10240 * 8 * 128, f4, p4)
+    assert bs == 48_906_240
