@@ -17,6 +17,7 @@ from .ragged_attn import (  # noqa: F401
     ragged_attention_sibling_with_lse,
     ragged_attention_with_lse,
     ragged_attention_with_parents,
+    set_layout_copies,
 )
 
 __version__ = "0.1.0"

@@ -15,7 +15,10 @@ Differences from the reference, all supersets:
     h // (Hq // Hkv), exactly what repeat_kv would have produced.
   * Inputs whose last dim is not unit-stride or whose rows are not 16-byte
     aligned are copied to a contiguous layout first (the reference accepts any
-    strides; the HIP kernels read 16-byte vectors).
+    strides; the HIP kernels read 16-byte vectors).  Such a copy is the only
+    allocation a call makes besides its outputs and workspace (under graph
+    capture it comes from the graph's pool); set_layout_copies(False) makes
+    those inputs raise ValueError instead.
   * bf16 runs natively (the reference casts bf16 to fp16 below SM 8.9,
     src/ragged_attn.py:1118-1127; gfx950 has bf16 dot/MFMA instructions).
 """
@@ -55,8 +58,27 @@ def _vec_ok(t: torch.Tensor) -> bool:
     return st[-1] == 1 and all(s % 8 == 0 for s in st[:-1]) and t.data_ptr() % 16 == 0
 
 
+_LAYOUT_COPIES = [True]
+
+
+def set_layout_copies(allowed: bool) -> bool:
+    """Whether inputs the kernels cannot read as 16-byte rows are copied to a
+    contiguous layout (True, the default: any strides work, as in the
+    reference) or rejected with ValueError (False: a call then never allocates
+    beyond its outputs and workspace).  Returns the previous setting."""
+    prev = _LAYOUT_COPIES[0]
+    _LAYOUT_COPIES[0] = bool(allowed)
+    return prev
+
+
 def _vec(t: torch.Tensor) -> torch.Tensor:
-    return t if _vec_ok(t) else t.contiguous()
+    if _vec_ok(t):
+        return t
+    if not _LAYOUT_COPIES[0]:
+        raise ValueError(f"tensor of shape {tuple(t.shape)} and strides {tuple(t.stride())} is not readable as "
+                         "16-byte rows (unit last stride, 8-element aligned strides, 16-byte aligned base) and "
+                         "layout copies are off (set_layout_copies)")
+    return t.contiguous()
 
 
 def _require_device(*ts):

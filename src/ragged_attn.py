@@ -15,4 +15,5 @@ from qattention_amd.ragged_attn import (  # noqa: F401
     ragged_attention_with_lse,
     ragged_attention_with_parents,
     ragged_tree_attn,
+    set_layout_copies,
 )

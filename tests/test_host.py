@@ -295,3 +295,27 @@ def test_src_shim_reexports():
                  "ragged_attention_paged", "build_paged_kv", "fused_lse_merge", "ragged_tree_attn"):
         assert getattr(sra, name) is getattr(ra, name)
     assert stm.tree_attention_mask is tm.tree_attention_mask
+
+
+def test_layout_copies_switch():
+    """Inputs the kernels cannot read as 16-byte rows are copied by default
+    (any strides work, as in the reference); with set_layout_copies(False)
+    they raise instead, so a call allocates nothing beyond its outputs."""
+    import torch
+    from qattention_amd import ragged_attn as ra
+
+    base = torch.zeros(16, 4, 130, dtype=torch.float16)
+    ok = base[:, :, :128]              # outer strides 520 and 130: 130 % 8 != 0
+    assert not ra._vec_ok(ok)
+    assert ra._vec(ok).is_contiguous()
+    good = torch.zeros(16, 4, 128, dtype=torch.float16)
+    assert ra._vec(good) is good
+    prev = ra.set_layout_copies(False)
+    try:
+        assert prev is True
+        assert ra._vec(good) is good
+        with pytest.raises(ValueError, match="layout copies are off"):
+            ra._vec(ok)
+    finally:
+        ra.set_layout_copies(prev)
+    assert ra._vec(ok).is_contiguous()
