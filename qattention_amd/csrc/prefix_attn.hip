@@ -77,8 +77,19 @@ constexpr int kWaitVm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (
 // (lgkmcnt(0)) before each use of one.  The kernel orders these loads itself
 // (s_waitcnt vmcnt + barrier before a buffer is read, barrier before it is
 // overwritten).
+// RFL: take the base and destination through readfirstlane, for code where
+// the compiler cannot prove them wave-uniform on its own (each 32-bit half
+// widened as unsigned: readfirstlane returns int).
+template <bool RFL = false>
 __device__ __forceinline__ void lds_dma16(uint32_t voff, const char* sbase, void* dst) {
-    const uint32_t lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)dst;
+    uint32_t lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)dst;
+    if constexpr (RFL) {
+        const uint64_t a = (uint64_t)(uintptr_t)sbase;
+        const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)a);
+        const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(a >> 32));
+        sbase = (const char*)(uintptr_t)(((uint64_t)hi << 32) | (uint64_t)lo);
+        lds = (uint32_t)__builtin_amdgcn_readfirstlane((int)lds);
+    }
     asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds)
                  : "memory", "m0");
 }
@@ -87,9 +98,14 @@ __device__ __forceinline__ void lds_dma16(uint32_t voff, const char* sbase, void
 // none for the prefix-only pass); the split kernels leave the walk to the tree
 // kernels.  DBG: the walk-export instantiation (qattn_debug_walk), which also
 // writes each query's attended ancestors to tp.dbg_walk.
-template <typename T, int D, bool FUSED, bool LSE, int WALK, bool BATCH, bool DBG = false>
+// QB: 16-row column blocks per wave (2; 1 halves the query tile for calls
+// whose split units would leave CUs idle, split kernels only).
+template <typename T, int D, bool FUSED, bool LSE, int WALK, bool BATCH, bool DBG = false, int QB = 2>
 __global__ __launch_bounds__(kPrefixThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefix_attn_kernel(
     PrefixParams p, TreeParams tp) {
+    static_assert(QB == 2 || (QB == 1 && !FUSED), "the fused epilogue walks two column blocks per wave");
+    constexpr int kQB = QB;         // (hides the namespace default) column blocks per wave
+    constexpr int kBM = 64 * QB;    // query rows per workgroup
     constexpr int NC = D / 32;      // MFMA k-chunks over the head dim
     constexpr int ND = D / 16;      // output tiles over the head dim
     constexpr int DV = D / 8;       // 16-byte chunks per key row
@@ -201,7 +217,7 @@ __global__ __launch_bounds__(kPrefixThreads) __attribute__((amdgpu_waves_per_eu(
         const char* gb = base + (int64_t)kb * st;
         if (__builtin_expect(kb + kBN <= k_hi, 1)) {
 #pragma unroll
-            for (int i = 0; i < NI; ++i) lds_dma16(off[i], gb, buf + (wave * NI + i) * 512);
+            for (int i = 0; i < NI; ++i) lds_dma16<QB == 1>(off[i], gb, buf + (wave * NI + i) * 512);
         } else {
             // tail block of the split: rows past k_hi - 1 load that key instead
             const int last = k_hi - 1 - kb;
@@ -209,7 +225,7 @@ __global__ __launch_bounds__(kPrefixThreads) __attribute__((amdgpu_waves_per_eu(
             for (int i = 0; i < NI; ++i) {
                 const int row = (wave * NI + i) * RPI + lane / DV;
                 const uint32_t col = 16 * ((lane % DV) ^ kv_swz(row, DV));
-                lds_dma16((uint32_t)min(row, last) * (uint32_t)st + col, gb, buf + (wave * NI + i) * 512);
+                lds_dma16<QB == 1>((uint32_t)min(row, last) * (uint32_t)st + col, gb, buf + (wave * NI + i) * 512);
             }
         }
     };
@@ -695,8 +711,8 @@ static int run_prefix_merge(const TreeParams& p, int head_dim, hipStream_t st) {
 // ---------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------
-static int64_t units_per_split(int batch, int hkv, int max_seqlen, int group) {
-    const int64_t qtiles = ((int64_t)max_seqlen * group + kBM - 1) / kBM;
+static int64_t units_per_split(int batch, int hkv, int max_seqlen, int group, int bm = kBM) {
+    const int64_t qtiles = ((int64_t)max_seqlen * group + bm - 1) / bm;
     return (int64_t)batch * hkv * qtiles;
 }
 
@@ -731,7 +747,7 @@ static int64_t workspace_bytes(int64_t total_tokens, int hq, int head_dim, int s
 }
 
 template <typename T, int D, bool BATCH>
-static void launch_prefix_b(const PrefixParams& pp, const TreeParams& tp, bool fused, int walk, dim3 g,
+static void launch_prefix_b(const PrefixParams& pp, const TreeParams& tp, bool fused, bool half, int walk, dim3 g,
                             hipStream_t st) {
     const dim3 b(kPrefixThreads);
     if constexpr (T::kCode == QATTN_DTYPE_F16 && !BATCH) {
@@ -746,7 +762,10 @@ static void launch_prefix_b(const PrefixParams& pp, const TreeParams& tp, bool f
             return;
         }
     }
-    if (!fused)
+    if (!fused && half)
+        hipLaunchKernelGGL((prefix_attn_kernel<T, D, false, false, WALK_HEAP, BATCH, false, 1>), g, b, 0, st, pp,
+                           tp);
+    else if (!fused)
         hipLaunchKernelGGL((prefix_attn_kernel<T, D, false, false, WALK_HEAP, BATCH>), g, b, 0, st, pp, tp);
     else if (walk == WALK_NONE && tp.lse)
         hipLaunchKernelGGL((prefix_attn_kernel<T, D, true, true, WALK_NONE, BATCH>), g, b, 0, st, pp, tp);
@@ -763,7 +782,8 @@ static void launch_prefix_b(const PrefixParams& pp, const TreeParams& tp, bool f
 }
 
 template <typename T, int D>
-static int launch_prefix(const PrefixParams& pp, const TreeParams& tp, bool fused, int walk, hipStream_t st) {
+static int launch_prefix(const PrefixParams& pp, const TreeParams& tp, bool fused, bool half, int walk,
+                         hipStream_t st) {
     const int64_t grid = ((int64_t)pp.n_units + 7) / 8 * 8;
     if (grid >= (int64_t(1) << 31)) {
         set_error("prefix grid too large");
@@ -771,9 +791,9 @@ static int launch_prefix(const PrefixParams& pp, const TreeParams& tp, bool fuse
     }
     // (a null cu is a uniform batch: its addressing is compiled separately)
     if (pp.cu)
-        launch_prefix_b<T, D, false>(pp, tp, fused, walk, dim3((unsigned)grid), st);
+        launch_prefix_b<T, D, false>(pp, tp, fused, half, walk, dim3((unsigned)grid), st);
     else
-        launch_prefix_b<T, D, true>(pp, tp, fused, walk, dim3((unsigned)grid), st);
+        launch_prefix_b<T, D, true>(pp, tp, fused, half, walk, dim3((unsigned)grid), st);
     return launch_status("prefix_attn_kernel");
 }
 
@@ -907,18 +927,22 @@ static int prefix_tree_impl(const void* q, const int64_t q_stride[3], const void
     pp.L = prefix_len;
     pp.n_split = splits;
     pp.blocks_per_split = bps;
-    pp.qtiles = (int32_t)(((int64_t)max_seqlen * g + kBM - 1) / kBM);
-    pp.n_units = (int32_t)(ups * splits);
+    // Split units that would leave CUs idle (fewer than one per CU: a decode
+    // step of a small tree) take half-height query tiles, twice as many.
+    const bool half = !fused && ups * splits < 256;
+    const int bm = half ? kBM / 2 : kBM;
+    pp.qtiles = (int32_t)(((int64_t)max_seqlen * g + bm - 1) / bm);
+    pp.n_units = (int32_t)(units_per_split(batch, num_kv_heads, max_seqlen, g, bm) * splits);
     pp.gdiv = make_divider(g);
     pp.scale_log2 = scale * kLog2e;
     if (dtype == QATTN_DTYPE_F16) {
-        rc = head_dim == 32   ? launch_prefix<F16, 32>(pp, tp, fused, walk, st)
-             : head_dim == 64 ? launch_prefix<F16, 64>(pp, tp, fused, walk, st)
-                              : launch_prefix<F16, 128>(pp, tp, fused, walk, st);
+        rc = head_dim == 32   ? launch_prefix<F16, 32>(pp, tp, fused, half, walk, st)
+             : head_dim == 64 ? launch_prefix<F16, 64>(pp, tp, fused, half, walk, st)
+                              : launch_prefix<F16, 128>(pp, tp, fused, half, walk, st);
     } else {
-        rc = head_dim == 32   ? launch_prefix<BF16, 32>(pp, tp, fused, walk, st)
-             : head_dim == 64 ? launch_prefix<BF16, 64>(pp, tp, fused, walk, st)
-                              : launch_prefix<BF16, 128>(pp, tp, fused, walk, st);
+        rc = head_dim == 32   ? launch_prefix<BF16, 32>(pp, tp, fused, half, walk, st)
+             : head_dim == 64 ? launch_prefix<BF16, 64>(pp, tp, fused, half, walk, st)
+                              : launch_prefix<BF16, 128>(pp, tp, fused, half, walk, st);
     }
     if (rc || fused) return rc;
     tp.part_m = pp.part_m;
