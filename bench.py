@@ -525,6 +525,9 @@ def main():
                       "cfg4_ratio": round(us4 / us4p, 3),
                       "cfg4_frac": roofline_of(CONFIGS["cfg4"], us4)["frac"],
                       "cfg4_prefix_only_frac": roofline_of(CONFIGS["cfg4_prefix"], us4p)["frac"]})
+        # one EAGLE-3 verify step (latency-bound: a decode step of a small draft tree)
+        use3, _, _ = measure("eagle3", _lib.ALGO_AUTO, args.steps, args.warmup)
+        extra.update({"eagle3_us": round(use3, 2)})
 
     cpu = None
     if not args.no_cpu_baseline and layout not in ("merge", "prefix_only"):
