@@ -31,15 +31,20 @@ def _ra():
     return ragged_attn
 
 
-def _close(o, o_ref, dtype, what):
+def _close(o, o_ref, dtype, what, sigma=1.0):
+    # The bounds are stated for N(0, 1) inputs: 2e-3 absolute for fp16 (the
+    # north-star bound), relative where |O| > 1 (fp16 rounds O at 2^-11 of
+    # its magnitude).  Rounding errors scale with the size of the V rows an
+    # output mixes, not only with |O| (split states and P round before the
+    # weights cancel), so for inputs of scale sigma > 1 the absolute part
+    # scales with sigma.
+    s = max(1.0, sigma)
     if dtype == torch.float16:
-        # 2e-3 absolute (stated for N(0, 1) inputs),
-        # relative where |O| > 1: fp16 rounds O at 2^-11 of its magnitude
-        bound = 2e-3 * np.maximum(1.0, np.abs(o_ref))
+        bound = 2e-3 * np.maximum(s, np.abs(o_ref))
         err = np.abs(o - o_ref)
         assert (err <= bound).all(), f"{what}: max abs err {err.max():.3e}"
     else:
-        bound = 2.0 ** -7 * np.maximum(1.0, np.abs(o_ref)) + 1e-3
+        bound = 2.0 ** -7 * np.maximum(s, np.abs(o_ref)) + 1e-3 * s
         assert (np.abs(o - o_ref) <= bound).all(), f"{what}: bf16 err {np.abs(o - o_ref).max():.3e}"
 
 
@@ -138,7 +143,7 @@ def test_random_case(seed):
         LSE = L4.permute(0, 2, 1).reshape(B * N, Hq)
         o_ref, lse_ref, _ = oracle_tree(Q, K, V, cu, b, md, parents=None if par is None else np.tile(par, B),
                                         Kp=Kp if L else None, Vp=Vp if L else None)
-    _close(O.double().cpu().numpy(), o_ref, dtype, f"case {seed} ({path})")
+    _close(O.double().cpu().numpy(), o_ref, dtype, f"case {seed} ({path})", c["sigma"])
     if LSE is not None:
         err = float(np.abs(LSE.double().cpu().numpy() - lse_ref).max()) if LSE.numel() else 0.0
         assert err <= (1e-4 if dtype == torch.float16 else 1e-3) * max(1.0, c["sigma"] ** 2), \
