@@ -660,15 +660,15 @@ __global__ __launch_bounds__(kPrefixThreads) __attribute__((amdgpu_waves_per_eu(
 // Split merge of the prefix-only pass: 4 lanes per (token, q head) fold the
 // splits' partial states and store the normalised output (+ LSE).
 // ---------------------------------------------------------------------------
-template <typename T, int D, bool LSE, bool BATCH>
+// TPB: threads per workgroup (one wave when 256-thread workgroups would
+// occupy under half the CUs: four times the CUs then share the loads).
+template <typename T, int D, bool LSE, bool BATCH, int TPB = kPrefixThreads>
 __global__ __launch_bounds__(kPrefixThreads) void prefix_merge_kernel(TreeParams p) {
-    constexpr int SLOTS = kPrefixThreads / 4;
+    constexpr int SLOTS = TPB / 4;
     const int j = threadIdx.x & 3;
     const int64_t slot = (int64_t)blockIdx.x * SLOTS + (threadIdx.x >> 2);
-    const int h = (int)(slot % p.Hq);
-    const int64_t rest = slot / p.Hq;
-    const int tok = (int)(rest % p.max_seqlen);
-    const int seq = (int)(rest / p.max_seqlen);
+    int h, tok, seq;
+    slot_coords(p, slot, (int64_t)gridDim.x * SLOTS, h, tok, seq);
     if (seq >= p.B) return;
     int32_t start, n;
     if (!seq_bounds<BATCH>(p, seq, start, n)) return;
@@ -687,12 +687,17 @@ static int launch_prefix_merge(const TreeParams& p, hipStream_t st) {
         set_error("merge grid too large (%lld blocks)", (long long)blocks);
         return QATTN_ERR_ARG;
     }
-    if (p.lse)
-        hipLaunchKernelGGL((prefix_merge_kernel<T, D, true, BATCH>), dim3((unsigned)blocks), dim3(kPrefixThreads), 0,
-                           st, p);
+    const dim3 g((unsigned)blocks), b(kPrefixThreads);
+    const bool small = blocks < 128;  // under half the CUs: one-wave workgroups instead
+    const dim3 g1((unsigned)(blocks * (kPrefixThreads / 64))), b1(64);
+    if (p.lse && small)
+        hipLaunchKernelGGL((prefix_merge_kernel<T, D, true, BATCH, 64>), g1, b1, 0, st, p);
+    else if (p.lse)
+        hipLaunchKernelGGL((prefix_merge_kernel<T, D, true, BATCH>), g, b, 0, st, p);
+    else if (small)
+        hipLaunchKernelGGL((prefix_merge_kernel<T, D, false, BATCH, 64>), g1, b1, 0, st, p);
     else
-        hipLaunchKernelGGL((prefix_merge_kernel<T, D, false, BATCH>), dim3((unsigned)blocks), dim3(kPrefixThreads),
-                           0, st, p);
+        hipLaunchKernelGGL((prefix_merge_kernel<T, D, false, BATCH>), g, b, 0, st, p);
     return launch_status("prefix_merge_kernel");
 }
 

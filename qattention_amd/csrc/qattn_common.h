@@ -69,6 +69,7 @@ struct TreeParams {
     int32_t B, Hq, Hkv, group, max_seqlen, max_depth;
     Divider bdiv;               // branching factor
     Divider pdiv;               // paged K/V: page_size
+    Divider hqdiv, msdiv;       // Hq and max_seqlen (>= 1): the gather kernel's slot decomposition
     float scale_log2;           // softmax scale * log2(e)
     // split-K prefix partial state merged into the tree state (may be null)
     const float* part_m;        // [n_split][T][Hq]   running max (log2 domain)

@@ -56,10 +56,16 @@ static thread_local int32_t* g_dbg_walk = nullptr;
 // ---------------------------------------------------------------------------
 // DBG: the walk-export instantiation (qattn_debug_walk): every query's walk
 // steps are also written to p.dbg_walk.
-template <typename T, int D, int WALK, int LAYOUT, bool LSE, bool PSTATE, bool BATCH, bool DBG = false>
+// TPB: threads per workgroup.  A split merge that would occupy under half
+// the CUs (a decode step of a small tree) takes one wave per workgroup
+// instead, so four times the CUs share its loads (each CU's vector memory
+// path, not latency, bounds such a launch: the EAGLE-3 step's merge of 8
+// states over 30 workgroups, 18.62 -> 17.12 us per call).
+template <typename T, int D, int WALK, int LAYOUT, bool LSE, bool PSTATE, bool BATCH, bool DBG = false,
+          int TPB = kThreads>
 __global__ __launch_bounds__(kThreads) void tree_gather_kernel(TreeParams p) {
     constexpr int NCH = D / 32;
-    constexpr int SLOTS = kThreads / 4;
+    constexpr int SLOTS = TPB / 4;
     const int j = threadIdx.x & 3;
     // Without split states: XCD-contiguous block order.  The dispatcher
     // places block i on XCD i % 8, so XCD x takes the x-th eighth of the
@@ -73,10 +79,8 @@ __global__ __launch_bounds__(kThreads) void tree_gather_kernel(TreeParams p) {
         lbk = x * per + min(x, rem) + (bx >> 3);
     }
     const int64_t slot = (int64_t)lbk * SLOTS + (threadIdx.x >> 2);
-    const int h = (int)(slot % p.Hq);
-    const int64_t rest = slot / p.Hq;
-    const int tok = (int)(rest % p.max_seqlen);
-    const int seq = (int)(rest / p.max_seqlen);
+    int h, tok, seq;
+    slot_coords(p, slot, (int64_t)gridDim.x * SLOTS, h, tok, seq);
     if (seq >= p.B) return;
     int32_t start, n;
     if (!seq_bounds<BATCH>(p, seq, start, n)) return;
@@ -328,6 +332,14 @@ static int launch_gather(const TreeParams& p, hipStream_t st) {
         set_error("grid too large (%lld blocks)", (long long)blocks);
         return QATTN_ERR_ARG;
     }
+    if constexpr (PSTATE && LAYOUT == KV_PACKED && !DBG) {
+        if (blocks < 128) {  // (cfg4's merge, 170 workgroups, timed within noise either way)
+            constexpr int S1 = 64 / 4;
+            hipLaunchKernelGGL((tree_gather_kernel<T, D, WALK, LAYOUT, LSE, PSTATE, BATCH, DBG, 64>),
+                               dim3((unsigned)((slots + S1 - 1) / S1)), dim3(64), 0, st, p);
+            return launch_status("tree_gather_kernel");
+        }
+    }
     hipLaunchKernelGGL((tree_gather_kernel<T, D, WALK, LAYOUT, LSE, PSTATE, BATCH, DBG>), dim3((unsigned)blocks),
                        dim3(kThreads), 0, st, p);
     return launch_status("tree_gather_kernel");
@@ -473,6 +485,8 @@ int fill_tree_params(TreeParams& p, const void* q, const int64_t* qs, const void
     p.max_seqlen = max_seqlen;
     p.max_depth = max_depth;
     p.bdiv = make_divider(b);
+    p.hqdiv = make_divider(hq);
+    p.msdiv = make_divider(max_seqlen > 0 ? max_seqlen : 1);
     p.scale_log2 = scale * kLog2e;
     p.dbg_walk = g_dbg_walk;
     return QATTN_OK;

@@ -64,6 +64,26 @@ __device__ __forceinline__ int32_t walk_next(const TreeParams& p, int32_t pb, in
     }
 }
 
+// A (token, q head) slot of the 4-lanes-per-query kernels (q head fastest)
+// as q head, token and sequence: 32-bit magic-number divisions (the 64-bit
+// divisions held a small launch's first loads back by ~0.5 us) whenever the
+// grid's slots fit in 31 bits (wave-uniform), else 64-bit.
+__device__ __forceinline__ void slot_coords(const TreeParams& p, int64_t slot, int64_t nslots, int& h, int& tok,
+                                            int& seq) {
+    if (nslots < (int64_t(1) << 31)) {
+        const int32_t s32 = (int32_t)slot;
+        const int32_t r = divide(s32, p.hqdiv);
+        h = s32 - r * p.Hq;
+        seq = divide(r, p.msdiv);
+        tok = r - seq * p.max_seqlen;
+    } else {
+        h = (int)(slot % p.Hq);
+        const int64_t rest = slot / p.Hq;
+        tok = (int)(rest % p.max_seqlen);
+        seq = (int)(rest / p.max_seqlen);
+    }
+}
+
 // Q fragment of a query in the 4-lane layout.
 template <int D, bool BATCH = false>
 __device__ __forceinline__ void load_q4(const TreeParams& p, int seq, int64_t qrow, int h, int j, Vec16* qf) {
@@ -80,7 +100,10 @@ __device__ __forceinline__ void load_q4(const TreeParams& p, int seq, int64_t qr
 // are folded in batches of SP whose loads are issued together, each batch
 // moving the running maximum once (an online merge: no separate pass for the
 // maxima), so n splits cost about n / SP memory round trips.
-template <typename T, int D>
+// SPX: splits per batch of loads (0: the default below); 8 for launches of at
+// most one workgroup per CU, where registers are plentiful and each batch
+// is a full memory round trip.
+template <typename T, int D, int SPX = 0>
 __device__ __forceinline__ void load_partial_state4(const TreeParams& p, int64_t qrow, int h, int j,
                                                     float& m, float& l, float* acc) {
     constexpr int NCH = D / 32;
@@ -88,7 +111,7 @@ __device__ __forceinline__ void load_partial_state4(const TreeParams& p, int64_t
     constexpr int W = H ? 1 : 2;  // 16-byte loads per 8-element chunk
     // splits per batch: 4 (fp16 states) or 3 (fp32) at head_dim 128; 6 fp16
     // states per batch needed more than 256 VGPRs in the gather kernel
-    constexpr int SP = (H && NCH == 4) ? 4 : 12 / NCH;
+    constexpr int SP = SPX > 0 ? SPX : ((H && NCH == 4) ? 4 : 12 / NCH);
     const int ns = p.n_split;
     const int64_t plane = p.total_tokens * (int64_t)p.Hq;
     const int64_t idx = qrow * p.Hq + h;
