@@ -732,8 +732,8 @@ static int prefix_splits(int64_t ups, int L, int num_splits, int& blocks_per_spl
         // few query rows (one decode step of a small tree) that traffic and the
         // per-split overheads outgrow the split's own work.  Keep at least an
         // eighth of the blocks, within 2..8, per split (one EAGLE-3 step over
-        // a 2048-token cache runs 18.6 us per call with 8 splits, 20.1 with 4,
-        // 22.8 with 16).
+        // a 2048-token cache runs 17.2 us per call with 8 splits, 18.8 with 4,
+        // 21.5 with 16).
         const int bps_min = std::min(8, std::max(2, blocks / 8));
         s = std::min(s, std::max(1, blocks / bps_min));
     }
