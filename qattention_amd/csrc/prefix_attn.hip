@@ -50,6 +50,7 @@ struct PrefixParams {
     int32_t B, Hq, Hkv, group, max_seqlen, L;
     int32_t n_split, blocks_per_split, qtiles, n_units;
     Divider gdiv;
+    Divider qtdiv, nsdiv, hkvdiv;  // qtiles, n_split, Hkv: the unit decode
     float scale_log2;
     int64_t sq_b;  // uniform batch only: per-sequence q offset (as TreeParams::sq_b)
 };
@@ -132,12 +133,14 @@ __global__ __launch_bounds__(kPrefixThreads) __attribute__((amdgpu_waves_per_eu(
     const int per = gridDim.x >> 3;
     const int unit = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
     if (unit >= p.n_units) return;
-    const int qt = unit % p.qtiles;
-    int r = unit / p.qtiles;
-    const int split = r % p.n_split;
-    r /= p.n_split;
-    const int kvh = r % p.Hkv;
-    const int seq = r / p.Hkv;
+    // (magic-number divisions: the generic 32-bit ones held the first loads
+    // of a short launch back)
+    const int r0 = divide(unit, p.qtdiv);
+    const int qt = unit - r0 * p.qtiles;
+    const int r1 = divide(r0, p.nsdiv);
+    const int split = r0 - r1 * p.n_split;
+    const int seq = divide(r1, p.hkvdiv);
+    const int kvh = r1 - seq * p.Hkv;
 
     // (BATCH: a uniform batch of max_seqlen rows per sequence, no cu)
     const int32_t s0 = BATCH ? seq * p.max_seqlen : p.cu[seq];
@@ -939,6 +942,9 @@ static int prefix_tree_impl(const void* q, const int64_t q_stride[3], const void
     pp.qtiles = (int32_t)(((int64_t)max_seqlen * g + bm - 1) / bm);
     pp.n_units = (int32_t)(units_per_split(batch, num_kv_heads, max_seqlen, g, bm) * splits);
     pp.gdiv = make_divider(g);
+    pp.qtdiv = make_divider(pp.qtiles);
+    pp.nsdiv = make_divider(splits);
+    pp.hkvdiv = make_divider(num_kv_heads);
     pp.scale_log2 = scale * kLog2e;
     if (dtype == QATTN_DTYPE_F16) {
         rc = head_dim == 32   ? launch_prefix<F16, 32>(pp, tp, fused, half, walk, st)
