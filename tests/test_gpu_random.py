@@ -19,7 +19,7 @@ pytestmark = pytest.mark.gpu
 
 DEV = "cuda"
 PATHS = ("heap", "parents", "paged", "prefix", "verify")
-CASES = 96
+CASES = 256
 
 
 def say(*a):
