@@ -100,10 +100,7 @@ __device__ __forceinline__ void load_q4(const TreeParams& p, int seq, int64_t qr
 // are folded in batches of SP whose loads are issued together, each batch
 // moving the running maximum once (an online merge: no separate pass for the
 // maxima), so n splits cost about n / SP memory round trips.
-// SPX: splits per batch of loads (0: the default below); 8 for launches of at
-// most one workgroup per CU, where registers are plentiful and each batch
-// is a full memory round trip.
-template <typename T, int D, int SPX = 0>
+template <typename T, int D>
 __device__ __forceinline__ void load_partial_state4(const TreeParams& p, int64_t qrow, int h, int j,
                                                     float& m, float& l, float* acc) {
     constexpr int NCH = D / 32;
@@ -111,7 +108,7 @@ __device__ __forceinline__ void load_partial_state4(const TreeParams& p, int64_t
     constexpr int W = H ? 1 : 2;  // 16-byte loads per 8-element chunk
     // splits per batch: 4 (fp16 states) or 3 (fp32) at head_dim 128; 6 fp16
     // states per batch needed more than 256 VGPRs in the gather kernel
-    constexpr int SP = SPX > 0 ? SPX : ((H && NCH == 4) ? 4 : 12 / NCH);
+    constexpr int SP = (H && NCH == 4) ? 4 : 12 / NCH;
     const int ns = p.n_split;
     const int64_t plane = p.total_tokens * (int64_t)p.Hq;
     const int64_t idx = qrow * p.Hq + h;
