@@ -16,12 +16,15 @@
  *   - an uncaptured launch uses the slot of its stream (launches on one
  *     stream run in order); 64 streams per device get a slot, launches on
  *     further streams run the static schedule;
- *   - a launch recorded into a graph keeps a slot of its own for every
- *     replay (replays of one graph executable run in order); after 192 such
- *     launches per device, further recorded launches use the static schedule.
+ *   - the launches recorded into a graph by one capture sequence on one
+ *     stream share a slot for every replay (they run in order, and replays
+ *     of one graph executable run in order); 192 such slots per device are
+ *     held at a time, each until its graph and the executables made from it
+ *     are destroyed; beyond that, recorded launches use the static schedule.
  *     As with any memory a capture records, two graph executables
  *     instantiated from one capture must not run at the same time.
- * Calls are thread-safe (the slot table is guarded by a mutex).
+ * qattn_sched_info() reports the slots in use and the launches that ran each
+ * schedule.  Calls are thread-safe (the slot table is guarded by a mutex).
  * Return value: QATTN_OK (0) or a negative QATTN_ERR_* code; the message of
  * the last failure on the calling thread is qattn_last_error().
  *
@@ -83,6 +86,17 @@ const char *qattn_version(void);
  * works, with the subtree kernel on its static schedule.
  */
 int qattn_init(void);
+
+/*
+ * Schedule-counter use on the CURRENT device (no reference counterpart: it
+ * makes the subtree kernel's schedule choice visible to tests and benchmarks).
+ * info[0] streams holding an eager slot, info[1] graph-capture slots held,
+ * info[2] subtree launches (eager or recorded) given counters, info[3]
+ * launches that wanted counters and ran the static schedule because no slot
+ * was free (launches before qattn_init are not counted), info[4] and info[5]
+ * the eager and captured slot capacities.
+ */
+int qattn_sched_info(int64_t info[6]);
 
 /* Message of the last failed call on this thread ("" if none). */
 const char *qattn_last_error(void);
@@ -181,7 +195,8 @@ int qattn_ancestors(const int32_t *cu_seqlens, const int32_t *parents, int32_t b
  * LDS row each step reads.  -2 at step 0 marks an inconsistency (a mask bit
  * on a row without a node, two rows at one step, a Q row staged from another
  * query).  Entries of queries no kernel computes are left as they were.
- * Only fp16 calls over packed cu_seqlens without LSE (else QATTN_ERR_ARG);
+ * Calls over packed cu_seqlens, fp16 or bf16, with or without lse (the
+ * uniform-batch qattn_ragged_tree_attn_fwd returns QATTN_ERR_ARG);
  * out is a DEVICE int32 array of total_tokens * num_q_heads * (max_depth+1)
  * entries.  NULL turns it off.
  */

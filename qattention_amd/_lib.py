@@ -39,6 +39,7 @@ SIGNATURES = {
     "qattn_version": (C.c_char_p, []),
     "qattn_last_error": (C.c_char_p, []),
     "qattn_init": (C.c_int, []),
+    "qattn_sched_info": (C.c_int, [_i64p]),
     "qattn_debug_walk": (C.c_int, [_p]),
     "qattn_tree_fwd": (C.c_int, [
         _p, _i64p, _p, _i64p, _p, _i64p, _p, _i64p, _p, _i64p,
@@ -124,6 +125,18 @@ def debug_walk(table):
         yield table
     finally:
         lib().qattn_debug_walk(None)
+
+
+def sched_info(device=None) -> dict:
+    """Schedule-counter use on a device (qattn_sched_info): slots held and
+    how many subtree launches ran with counters or fell back to the static
+    schedule."""
+    arr = (C.c_int64 * 6)()
+    with torch.cuda.device(device if device is not None else torch.cuda.current_device()):
+        check(lib().qattn_sched_info(arr), "qattn_sched_info")
+    keys = ("stream_slots", "capture_slots", "dynamic_launches", "static_launches",
+            "stream_capacity", "capture_capacity")
+    return dict(zip(keys, [int(x) for x in arr]))
 
 
 def last_error() -> str:

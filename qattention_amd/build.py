@@ -40,6 +40,9 @@ def compile_flags() -> list:
         # answer at once, where the subtree kernel overlaps it with its loads
         "-Xarch_device", "-mllvm=-amdgpu-atomic-optimizer-strategy=None",
         "-Wall", "-Wno-unused-function",
+        # inline assembly must not clobber registers the compiler reserves
+        # (M0, EXEC, VCC): such an asm statement is undefined behaviour
+        "-Werror=inline-asm",
     ]
 
 

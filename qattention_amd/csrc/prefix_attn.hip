@@ -91,8 +91,9 @@ __device__ __forceinline__ void lds_dma16(uint32_t voff, const char* sbase, void
         sbase = (const char*)(uintptr_t)(((uint64_t)hi << 32) | (uint64_t)lo);
         lds = (uint32_t)__builtin_amdgcn_readfirstlane((int)lds);
     }
-    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds)
-                 : "memory", "m0");
+    // M0 (the LDS destination) is an operand the compiler allocates ("{m0}"),
+    // so it writes M0 itself and knows its value afterwards
+    asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(lds) : "memory");
 }
 
 // WALK: the tree walk of the fused epilogue (heap or explicit parents, or
@@ -747,26 +748,34 @@ static int prefix_splits(int64_t ups, int L, int num_splits, int& blocks_per_spl
 
 static int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
 
-static int64_t workspace_bytes(int64_t total_tokens, int hq, int head_dim, int splits) {
+// Split-state bytes: m and l in fp32, the numerator in fp16 for fp16 inputs
+// (half_acc, kPartHalf) and fp32 otherwise.  qattn_prefix_workspace_bytes,
+// which takes no dtype, reports the fp32 size, an upper bound for both.
+static int64_t workspace_bytes(int64_t total_tokens, int hq, int head_dim, int splits, bool half_acc = false) {
     if (splits <= 1) return 0;  // one split: fused epilogue, no partial states
     const int64_t plane = total_tokens * hq;
-    // (m, l and the numerator in fp32: the bf16 layout; fp16 uses half of the last)
-    return 2 * align256(splits * plane * 4) + align256(splits * plane * head_dim * 4);
+    return 2 * align256(splits * plane * 4) + align256(splits * plane * head_dim * (half_acc ? 2 : 4));
 }
 
 template <typename T, int D, bool BATCH>
 static void launch_prefix_b(const PrefixParams& pp, const TreeParams& tp, bool fused, bool half, int walk, dim3 g,
                             hipStream_t st) {
     const dim3 b(kPrefixThreads);
-    if constexpr (T::kCode == QATTN_DTYPE_F16 && !BATCH) {
-        // walk export (the caller has checked: fp16, packed, no LSE)
-        if (fused && tp.dbg_walk && walk == WALK_HEAP) {
-            hipLaunchKernelGGL((prefix_attn_kernel<F16, D, true, false, WALK_HEAP, false, true>), g, b, 0, st, pp, tp);
-            return;
-        }
-        if (fused && tp.dbg_walk && walk == WALK_PARENTS) {
-            hipLaunchKernelGGL((prefix_attn_kernel<F16, D, true, false, WALK_PARENTS, false, true>), g, b, 0, st, pp,
-                               tp);
+    if constexpr (!BATCH) {
+        // walk export of the fused epilogue (the caller has checked: packed cu_seqlens)
+        if (fused && tp.dbg_walk && (walk == WALK_HEAP || walk == WALK_PARENTS)) {
+            if (walk == WALK_HEAP && tp.lse)
+                hipLaunchKernelGGL((prefix_attn_kernel<T, D, true, true, WALK_HEAP, false, true>), g, b, 0, st, pp,
+                                   tp);
+            else if (walk == WALK_HEAP)
+                hipLaunchKernelGGL((prefix_attn_kernel<T, D, true, false, WALK_HEAP, false, true>), g, b, 0, st, pp,
+                                   tp);
+            else if (tp.lse)
+                hipLaunchKernelGGL((prefix_attn_kernel<T, D, true, true, WALK_PARENTS, false, true>), g, b, 0, st,
+                                   pp, tp);
+            else
+                hipLaunchKernelGGL((prefix_attn_kernel<T, D, true, false, WALK_PARENTS, false, true>), g, b, 0, st,
+                                   pp, tp);
             return;
         }
     }
@@ -891,7 +900,7 @@ static int prefix_tree_impl(const void* q, const int64_t q_stride[3], const void
     int bps = 0;
     const int64_t ups = units_per_split(batch, num_kv_heads, max_seqlen, g);
     const int splits = prefix_splits(ups, prefix_len, num_splits, bps);
-    const int64_t need = workspace_bytes(total_tokens, num_q_heads, head_dim, splits);
+    const int64_t need = workspace_bytes(total_tokens, num_q_heads, head_dim, splits, dtype == QATTN_DTYPE_F16);
     if (need > 0 && (!workspace || workspace_size < need || ((uintptr_t)workspace & 255))) {
         set_error("workspace of %lld bytes (256-byte aligned) required, got %lld", (long long)need,
                   (long long)workspace_size);
@@ -902,8 +911,8 @@ static int prefix_tree_impl(const void* q, const int64_t q_stride[3], const void
         return QATTN_ERR_ARG;
     }
     const bool fused = splits == 1;
-    if (tp.dbg_walk && (dtype != QATTN_DTYPE_F16 || lse || !tp.cu)) {
-        set_error("the walk export runs fp16 calls over packed cu_seqlens without LSE");
+    if (tp.dbg_walk && !tp.cu) {
+        set_error("the walk export runs calls over packed cu_seqlens");
         return QATTN_ERR_ARG;
     }
     const int64_t plane = total_tokens * num_q_heads;
@@ -1079,6 +1088,20 @@ int qattn_init(void) {
     return scratch_ptr() ? QATTN_OK : QATTN_ERR_HIP;
 }
 
+int qattn_sched_info(int64_t info[6]) {
+    clear_error();
+    if (!info) {
+        set_error("info is null");
+        return QATTN_ERR_ARG;
+    }
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess) {
+        set_error("hipGetDevice failed");
+        return QATTN_ERR_HIP;
+    }
+    return sched_info(dev, info);
+}
+
 int64_t qattn_prefix_workspace_bytes(int32_t batch, int32_t max_seqlen, int64_t total_tokens, int32_t num_q_heads,
                                      int32_t num_kv_heads, int32_t head_dim, int32_t prefix_len, int32_t num_splits) {
     if (batch <= 0 || max_seqlen <= 0 || total_tokens <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 ||
@@ -1175,13 +1198,15 @@ int qattn_ragged_tree_attn_fwd_noalloc(const void* q, const int64_t q_stride[4],
         const int64_t ups = units_per_split(batch, num_kv_heads, num_tree, num_q_heads / num_kv_heads);
         int bps = 0;
         int s = prefix_splits(ups, num_prefix, num_splits, bps);
-        if (workspace_bytes(total, num_q_heads, head_dim, s) > kScratchBytes) {
+        const bool half = dtype == QATTN_DTYPE_F16;  // fp16 split numerators (kPartHalf)
+        if (workspace_bytes(total, num_q_heads, head_dim, s, half) > kScratchBytes) {
             if (num_splits > 0) {
-                set_error("%d prefix splits need %lld bytes of split state; the scratch array holds %lld",
-                          s, (long long)workspace_bytes(total, num_q_heads, head_dim, s), (long long)kScratchBytes);
+                set_error("%d prefix splits need %lld bytes of split state; the scratch array holds %lld", s,
+                          (long long)workspace_bytes(total, num_q_heads, head_dim, s, half),
+                          (long long)kScratchBytes);
                 return QATTN_ERR_WORKSPACE;
             }
-            while (s > 1 && workspace_bytes(total, num_q_heads, head_dim, s) > kScratchBytes) --s;
+            while (s > 1 && workspace_bytes(total, num_q_heads, head_dim, s, half) > kScratchBytes) --s;
             num_splits = s;
         }
     }

@@ -157,6 +157,8 @@ int launch_stream(const TreeParams& p, const SubtreePlan& plan, int dtype, int h
 // qattn_init's part for the subtree kernel: the device address of the
 // current device's counter pool, zeroed (synchronously, on a private stream).
 int sched_init(int dev);
+// qattn_sched_info's figures for device dev (see include/qattn.h).
+int sched_info(int dev, int64_t info[6]);
 
 void set_error(const char* fmt, ...);
 void clear_error();

@@ -928,23 +928,53 @@ __attribute__((amdgpu_waves_per_eu(3, 3))) void tree_stream_kernel(
 //  * an eager launch takes the slot of its stream (launches on one stream run
 //    in order; the first kSchedStreamSlots streams seen on a device get one
 //    each, later streams run the static schedule);
-//  * a launch recorded into a graph keeps a slot of its own for every replay
-//    (replays of one graph executable run in order); when the recorded slots
-//    run out the launch is recorded with the static schedule.
+//  * launches recorded into a graph share one slot per (capture sequence,
+//    capturing stream): they form a chain of the graph, which runs in order,
+//    and replays of one graph executable run in order.  The slot goes back to
+//    the pool when the graph and every executable made from it are destroyed
+//    (a HIP user object that the graph retains; the runtime releases it once
+//    the pending replays are done).  When the captured slots run out, the
+//    launch is recorded with the static schedule.
 // Before qattn_init has run on a device every launch uses the static schedule
 // (same results, slower): the library never allocates, zeroes or
-// synchronises behind a call.
-constexpr int kSchedStreamSlots = 64, kSchedMaxDev = 64;
+// synchronises behind a call.  qattn_sched_info reports the slots in use and
+// how many launches ran each schedule.
+constexpr int kSchedStreamSlots = 64, kSchedCapSlots = kSchedSlots - kSchedStreamSlots, kSchedMaxDev = 64;
 static __device__ __align__(256) uint32_t sched_pool[kSchedGroups * kSchedStride];
 
 namespace {
+struct CapSlot {
+    unsigned long long id = 0;  // capture sequence
+    hipStream_t stream = nullptr;
+    bool used = false;
+};
 struct SchedDevice {
     uint32_t* pool = nullptr;  // device address of this device's sched_pool
     hipStream_t streams[kSchedStreamSlots] = {};
-    int n_streams = 0, captured_next = 0;
+    int n_streams = 0;
+    CapSlot cap[kSchedCapSlots];
+    int64_t dyn_launches = 0, static_launches = 0;
 };
 std::mutex g_sched_mu;
 SchedDevice g_sched[kSchedMaxDev];
+
+// What a captured slot's user object carries to its destructor.
+struct CapToken {
+    int dev, slot;
+    unsigned long long id;
+};
+
+// Destructor of a captured slot's user object (run by the HIP runtime once
+// the graph that retained it, and the executables made from it, are gone).
+void release_cap_slot(void* arg) {
+    CapToken* tk = static_cast<CapToken*>(arg);
+    {
+        std::lock_guard<std::mutex> lock(g_sched_mu);
+        CapSlot& cs = g_sched[tk->dev].cap[tk->slot];
+        if (cs.used && cs.id == tk->id) cs = CapSlot{};
+    }
+    delete tk;
+}
 }  // namespace
 
 int sched_init(int dev) {
@@ -976,27 +1006,87 @@ int sched_init(int dev) {
     return QATTN_OK;
 }
 
+int sched_info(int dev, int64_t info[6]) {
+    if (dev < 0 || dev >= kSchedMaxDev) {
+        set_error("device %d beyond the %d devices the library tracks", dev, kSchedMaxDev);
+        return QATTN_ERR_ARG;
+    }
+    std::lock_guard<std::mutex> lock(g_sched_mu);
+    const SchedDevice& sd = g_sched[dev];
+    int held = 0;
+    for (const CapSlot& c : sd.cap) held += c.used ? 1 : 0;
+    info[0] = sd.n_streams;
+    info[1] = held;
+    info[2] = sd.dyn_launches;
+    info[3] = sd.static_launches;
+    info[4] = kSchedStreamSlots;
+    info[5] = kSchedCapSlots;
+    return QATTN_OK;
+}
+
+// The counter slot of a launch on stream st, or null (static schedule).
 static uint32_t* sched_counters(int dev, hipStream_t st) {
     if (dev < 0 || dev >= kSchedMaxDev) return nullptr;
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-    if (hipStreamIsCapturing(st, &cs) != hipSuccess) return nullptr;
-    std::lock_guard<std::mutex> lock(g_sched_mu);
-    SchedDevice& sd = g_sched[dev];
-    if (!sd.pool) return nullptr;
+    unsigned long long cid = 0;
+    hipGraph_t graph = nullptr;
+    if (hipStreamGetCaptureInfo_v2(st, &cs, &cid, &graph) != hipSuccess) return nullptr;
+    const bool captured = cs != hipStreamCaptureStatusNone;
+    if (captured && cs != hipStreamCaptureStatusActive) return nullptr;
     int slot = -1;
-    if (cs != hipStreamCaptureStatusNone) {
-        if (sd.captured_next >= kSchedSlots - kSchedStreamSlots) return nullptr;
-        slot = kSchedStreamSlots + sd.captured_next++;
-    } else {
-        for (int i = 0; i < sd.n_streams; ++i)
-            if (sd.streams[i] == st) slot = i;
+    bool fresh = false;
+    uint32_t* pool = nullptr;
+    {
+        std::lock_guard<std::mutex> lock(g_sched_mu);
+        SchedDevice& sd = g_sched[dev];
+        if (!sd.pool) return nullptr;
+        pool = sd.pool;
+        if (captured) {
+            int free_slot = -1;
+            for (int i = 0; i < kSchedCapSlots && slot < 0; ++i) {
+                if (sd.cap[i].used && sd.cap[i].id == cid && sd.cap[i].stream == st) slot = i;
+                else if (!sd.cap[i].used && free_slot < 0) free_slot = i;
+            }
+            if (slot < 0 && free_slot >= 0) {
+                slot = free_slot;
+                sd.cap[slot].used = true;
+                sd.cap[slot].id = cid;
+                sd.cap[slot].stream = st;
+                fresh = true;
+            }
+            if (slot >= 0) slot += kSchedStreamSlots;
+        } else {
+            for (int i = 0; i < sd.n_streams; ++i)
+                if (sd.streams[i] == st) slot = i;
+            if (slot < 0 && sd.n_streams < kSchedStreamSlots) {
+                slot = sd.n_streams++;
+                sd.streams[slot] = st;
+            }
+        }
         if (slot < 0) {
-            if (sd.n_streams >= kSchedStreamSlots) return nullptr;
-            slot = sd.n_streams++;
-            sd.streams[slot] = st;
+            ++sd.static_launches;
+            return nullptr;
+        }
+        ++sd.dyn_launches;
+    }
+    if (fresh) {
+        // the graph being captured keeps the slot until it is destroyed (the
+        // HIP calls run outside the lock: the destructor takes it).  Without
+        // a user object the slot stays with this capture for the process's
+        // life, which is still correct.
+        CapToken* tk = new CapToken{dev, slot - kSchedStreamSlots, cid};
+        hipUserObject_t obj = nullptr;
+        if (hipUserObjectCreate(&obj, tk, release_cap_slot, 1, hipUserObjectNoDestructorSync) != hipSuccess) {
+            delete tk;
+        } else if (hipGraphRetainUserObject(graph, obj, 1, hipGraphUserObjectMove) != hipSuccess) {
+            (void)hipUserObjectRelease(obj, 1);  // runs the destructor: frees the slot
+            std::lock_guard<std::mutex> lock(g_sched_mu);
+            --g_sched[dev].dyn_launches;
+            ++g_sched[dev].static_launches;
+            return nullptr;
         }
     }
-    return sd.pool + 2 * slot;
+    return pool + 2 * slot;
 }
 
 template <typename T, int D, bool LSE, bool PSTATE, bool BATCH, bool DBG = false, bool PAGED = false>
@@ -1054,6 +1144,21 @@ static int launch_stream_t(const TreeParams& p, const SubtreePlan& plan, hipStre
     return launch_status("tree_stream_kernel");
 }
 
+// Walk export (qattn_debug_walk): the walk-export instantiation of the
+// kernel that serves the same call (dtype, LSE, prefix state, paged K/V).
+template <typename T, int D>
+static int launch_stream_dbg(const TreeParams& p, const SubtreePlan& plan, bool pstate, bool paged,
+                             hipStream_t st) {
+    if (p.lse) {
+        if (paged) return launch_stream_t<T, D, true, false, false, true, true>(p, plan, st);
+        return pstate ? launch_stream_t<T, D, true, true, false, true>(p, plan, st)
+                      : launch_stream_t<T, D, true, false, false, true>(p, plan, st);
+    }
+    if (paged) return launch_stream_t<T, D, false, false, false, true, true>(p, plan, st);
+    return pstate ? launch_stream_t<T, D, false, true, false, true>(p, plan, st)
+                  : launch_stream_t<T, D, false, false, false, true>(p, plan, st);
+}
+
 int launch_stream(const TreeParams& p, const SubtreePlan& plan, int dtype, int head_dim, bool pstate, bool paged,
                   hipStream_t st) {
     if (paged && (pstate || !p.cu)) {
@@ -1061,19 +1166,18 @@ int launch_stream(const TreeParams& p, const SubtreePlan& plan, int dtype, int h
         return QATTN_ERR_ARG;
     }
     if (p.dbg_walk) {
-        // walk export: fp16, packed cu_seqlens, no LSE (the walk does not depend on them)
-        if (dtype != QATTN_DTYPE_F16 || p.lse || !p.cu) {
-            set_error("the walk export runs fp16 calls over packed cu_seqlens without LSE");
+        // walk export: calls over packed cu_seqlens, either dtype, with or without LSE
+        if (!p.cu) {
+            set_error("the walk export runs calls over packed cu_seqlens");
             return QATTN_ERR_ARG;
         }
-#define QATTN_STREAM_DBG(D)                                                                        \
-    if (paged) return launch_stream_t<F16, D, false, false, false, true, true>(p, plan, st);       \
-    return pstate ? launch_stream_t<F16, D, false, true, false, true>(p, plan, st)                  \
-                  : launch_stream_t<F16, D, false, false, false, true>(p, plan, st);
-        if (head_dim == 32) { QATTN_STREAM_DBG(32) }
-        if (head_dim == 64) { QATTN_STREAM_DBG(64) }
-        QATTN_STREAM_DBG(128)
-#undef QATTN_STREAM_DBG
+        if (dtype == QATTN_DTYPE_F16)
+            return head_dim == 32   ? launch_stream_dbg<F16, 32>(p, plan, pstate, paged, st)
+                   : head_dim == 64 ? launch_stream_dbg<F16, 64>(p, plan, pstate, paged, st)
+                                    : launch_stream_dbg<F16, 128>(p, plan, pstate, paged, st);
+        return head_dim == 32   ? launch_stream_dbg<BF16, 32>(p, plan, pstate, paged, st)
+               : head_dim == 64 ? launch_stream_dbg<BF16, 64>(p, plan, pstate, paged, st)
+                                : launch_stream_dbg<BF16, 128>(p, plan, pstate, paged, st);
     }
 #define QATTN_STREAM_B(T, D, B)                                                                \
     if (p.lse) return pstate ? launch_stream_t<T, D, true, true, B>(p, plan, st)                \

@@ -332,7 +332,7 @@ static int launch_gather(const TreeParams& p, hipStream_t st) {
         set_error("grid too large (%lld blocks)", (long long)blocks);
         return QATTN_ERR_ARG;
     }
-    if constexpr (PSTATE && LAYOUT == KV_PACKED && !DBG) {
+    if constexpr (PSTATE && LAYOUT == KV_PACKED) {
         if (blocks < 128) {  // (cfg4's merge, 170 workgroups, timed within noise either way)
             constexpr int S1 = 64 / 4;
             hipLaunchKernelGGL((tree_gather_kernel<T, D, WALK, LAYOUT, LSE, PSTATE, BATCH, DBG, 64>),
@@ -353,6 +353,18 @@ static int gather_packed(const TreeParams& p, bool lse, bool pstate, hipStream_t
     }
     return lse ? launch_gather<T, D, WALK, KV_PACKED, true, false, BATCH>(p, st)
                : launch_gather<T, D, WALK, KV_PACKED, false, false, BATCH>(p, st);
+}
+
+// Walk export (qattn_debug_walk): the walk-export instantiation of the gather
+// kernel that serves the same call (dtype, LSE, walk, layout, prefix state).
+template <typename T, int D, bool LSE>
+static int gather_dbg(const TreeParams& p, int walk, int layout, bool pstate, hipStream_t st) {
+    if (layout == KV_PAGED) return launch_gather<T, D, WALK_HEAP, KV_PAGED, LSE, false, false, true>(p, st);
+    if (walk == WALK_HEAP)
+        return pstate ? launch_gather<T, D, WALK_HEAP, KV_PACKED, LSE, true, false, true>(p, st)
+                      : launch_gather<T, D, WALK_HEAP, KV_PACKED, LSE, false, false, true>(p, st);
+    return pstate ? launch_gather<T, D, WALK_PARENTS, KV_PACKED, LSE, true, false, true>(p, st)
+                  : launch_gather<T, D, WALK_PARENTS, KV_PACKED, LSE, false, false, true>(p, st);
 }
 
 template <typename T, int D>
@@ -393,17 +405,13 @@ static int dispatch_tree(const TreeParams& p, int walk, int layout, bool lse, bo
         return QATTN_ERR_ARG;
     }
     if (p.dbg_walk) {
-        // walk export: fp16, packed cu_seqlens, no LSE (the walk does not depend on them)
-        if (T::kCode != QATTN_DTYPE_F16 || lse || !p.cu) {
-            set_error("the walk export runs fp16 calls over packed cu_seqlens without LSE");
+        // walk export: calls over packed cu_seqlens, either dtype, with or without LSE
+        if (!p.cu) {
+            set_error("the walk export runs calls over packed cu_seqlens");
             return QATTN_ERR_ARG;
         }
-        if (layout == KV_PAGED) return launch_gather<F16, D, WALK_HEAP, KV_PAGED, false, false, false, true>(p, st);
-        if (walk == WALK_HEAP)
-            return pstate ? launch_gather<F16, D, WALK_HEAP, KV_PACKED, false, true, false, true>(p, st)
-                          : launch_gather<F16, D, WALK_HEAP, KV_PACKED, false, false, false, true>(p, st);
-        return pstate ? launch_gather<F16, D, WALK_PARENTS, KV_PACKED, false, true, false, true>(p, st)
-                      : launch_gather<F16, D, WALK_PARENTS, KV_PACKED, false, false, false, true>(p, st);
+        return lse ? gather_dbg<T, D, true>(p, walk, layout, pstate, st)
+                   : gather_dbg<T, D, false>(p, walk, layout, pstate, st);
     }
     if (layout == KV_PACKED) {
         // (a null cu is a uniform batch: its addressing is compiled separately)

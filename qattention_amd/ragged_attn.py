@@ -114,6 +114,25 @@ def _seqlens(cu_seqlens: torch.Tensor, B: int, device, max_seqlen: Optional[int]
     return max(int(max_seqlen), 0), cu_dev.contiguous()
 
 
+_ONE_SEQ_CU: dict = {}
+
+
+def _one_sequence_cu(T: int, device) -> torch.Tensor:
+    """Device cu_seqlens [0, T] for queries that form one sequence, made by
+    fill kernels (no host-to-device copy, so a call under graph capture
+    records it); kept per (device, T) when made outside capture."""
+    key = (device.index if device.index is not None else torch.cuda.current_device(), T)
+    cu = _ONE_SEQ_CU.get(key)
+    if cu is None:
+        cu = torch.full((2,), T, dtype=torch.int32, device=device)
+        cu[:1].fill_(0)  # (a fill kernel; `cu[0] = 0` would copy a host scalar)
+        if not torch.cuda.is_current_stream_capturing():
+            if len(_ONE_SEQ_CU) >= 256:
+                _ONE_SEQ_CU.clear()
+            _ONE_SEQ_CU[key] = cu
+    return cu
+
+
 def _heads(Q, K, V):
     T, Hq, D = Q.shape
     Hkv = K.shape[1]
@@ -522,7 +541,7 @@ def prefix_attention(
         K_prefix, V_prefix = K_prefix.unsqueeze(0), V_prefix.unsqueeze(0)
     Hkv = K_prefix.shape[2]
     if cu_seqlens is None:
-        cu_seqlens = torch.tensor([0, T], dtype=torch.int32, device=device)
+        cu_seqlens = _one_sequence_cu(T, device)  # capturable: no host copy
         max_seqlen = T
     B = int(cu_seqlens.shape[0]) - 1
     if (K_prefix.shape != V_prefix.shape or K_prefix.shape[3] != D or Hkv < 1 or Hq % Hkv

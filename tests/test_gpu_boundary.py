@@ -106,6 +106,32 @@ def test_prefix_attention_shared_prefix():
     assert np.abs(LSE.double().cpu().numpy() - lse_ref).max() <= 1e-4
 
 
+def test_prefix_attention_shared_prefix_graph_capture():
+    """The shared-prefix call (cu_seqlens None) records into a HIP graph: no
+    host copy inside the call.  A fresh query length (no cached cu) is
+    captured first, then replayed several times with eager calls and
+    synchronisations in between; every replay bit-equals the eager call."""
+    ra, _ = _ra()
+    T, H, D, L = 3 * 85 + 7, 8, 128, 1000
+    Q, _, _, _ = make_inputs([T], H, D, 8210)
+    Kp, Vp = _prefix(1, L, H, D, 8211)
+    Qd, Kd, Vd = Q.to(DEV), Kp[0].to(DEV), Vp[0].to(DEV)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        Og, LSEg = ra.prefix_attention(Qd, Kd, Vd)
+    O, LSE = ra.prefix_attention(Qd, Kd, Vd)
+    torch.cuda.synchronize()
+    for rep in range(3):
+        Og.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(Og, O) and torch.equal(LSEg, LSE), f"replay {rep}"
+        ra.prefix_attention(Qd, Kd, Vd)
+    o_ref, _ = _prefix_oracle(Q, torch.tensor([0, T], dtype=torch.int32), Kp, Vp)
+    check_fp16(O.double().cpu().numpy(), o_ref, "shared prefix, captured")
+
+
 @pytest.mark.parametrize("ns", [0, 1])
 def test_reference_pipeline_equals_verify(ns):
     """The reference's verify pipeline (scripts/benchmark_micro.py:568-593):
@@ -169,16 +195,32 @@ def test_tree_scale_any_sign(scale):
 # schedule-counter slots
 # ---------------------------------------------------------------------------
 
+def _hip_runtime():
+    """The HIP runtime torch has loaded (ctypes handle of the same mapping)."""
+    import ctypes
+    import os
+    maps = open(f"/proc/{os.getpid()}/maps").read()
+    paths = {l.split()[-1] for l in maps.splitlines() if "libamdhip64" in l}
+    assert len(paths) == 1, paths
+    hip = ctypes.CDLL(paths.pop())
+    hip.hipStreamCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+    hip.hipStreamDestroy.argtypes = [ctypes.c_void_p]
+    return hip
+
+
 def test_many_streams_match_solo():
     """Subtree-kernel launches (cfg2 shape: more tiles than workgroups, so
-    the counters are used) queued on 70 streams at once -- more than the 64
-    stream slots, so the last ones run the static schedule -- with several
+    the counters are used) queued on 72 distinct HIP streams at once (made
+    with hipStreamCreate: torch's own stream pool hands out at most 32
+    handles) -- more than the 64 stream slots, so the last ones run the
+    static schedule, which qattn_sched_info must count -- with several
     launches queued on the first stream before the others start, each
     bit-equal to a solo run of its inputs."""
+    import ctypes
     ra, _lib = _ra()
     B, b, d, H, D = 4, 4, 5, 32, 128
     N = num_tree_nodes(b, d)
-    nstreams, nsets = 70, 3
+    nstreams, nsets = 72, 3
     say("streams", nstreams)
     sets = []
     for i in range(nsets):
@@ -186,18 +228,105 @@ def test_many_streams_match_solo():
         sets.append((Q.to(DEV), K.to(DEV), V.to(DEV), cu.to(DEV)))
     solo = [ra._tree_forward(*s, b, d, N, False, _lib.ALGO_SUBTREE)[0] for s in sets]
     torch.cuda.synchronize()
-    streams = [torch.cuda.Stream() for _ in range(nstreams)]
-    outs = []
-    for i, s in enumerate(streams):
-        s.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(s):
-            reps = 6 if i == 0 else 1
-            for r in range(reps):
-                k = (i + r) % nsets
-                outs.append((k, ra._tree_forward(*sets[k], b, d, N, False, _lib.ALGO_SUBTREE)[0]))
+    hip = _hip_runtime()
+    handles = []
+    for _ in range(nstreams):
+        h = ctypes.c_void_p()
+        assert hip.hipStreamCreate(ctypes.byref(h)) == 0
+        handles.append(h.value)
+    assert len(set(handles)) == nstreams
+    before = _lib.sched_info()
+    try:
+        outs = []
+        for i, h in enumerate(handles):
+            s = torch.cuda.ExternalStream(h)
+            s.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(s):
+                reps = 6 if i == 0 else 1
+                for r in range(reps):
+                    k = (i + r) % nsets
+                    outs.append((k, ra._tree_forward(*sets[k], b, d, N, False, _lib.ALGO_SUBTREE)[0]))
+        torch.cuda.synchronize()
+        for k, o in outs:
+            assert torch.equal(o, solo[k]), f"set {k}"
+        after = _lib.sched_info()
+        say("sched_info", before, after)
+        assert after["stream_slots"] == after["stream_capacity"] == 64
+        # at least the streams beyond the 64 slots ran the static schedule
+        assert after["static_launches"] - before["static_launches"] >= nstreams - 64
+    finally:
+        torch.cuda.synchronize()
+        for h in handles:
+            hip.hipStreamDestroy(h)
+
+
+def test_graph_slots_per_capture_and_released():
+    """Launches recorded into graphs share one counter slot per capture: 10
+    graphs of 30 subtree launches (300 recorded launches, past the 192
+    captured slots the library holds) all run with counters, every replay
+    bit-equal to solo runs; destroying the graphs hands their slots back, so
+    200 more graphs captured and destroyed one after another still get
+    counters."""
+    import gc
+    import time
+    ra, _lib = _ra()
+    B, b, d, H, D = 4, 4, 5, 8, 128
+    N = num_tree_nodes(b, d)
+    ngraphs, per_graph, nsets = 10, 30, 3
+    say("graph slots", ngraphs, per_graph)
+    sets = []
+    for i in range(nsets):
+        Q, K, V, cu = tree_case(B, b, d, H, D, seed=9300 + i)
+        sets.append((Q.to(DEV), K.to(DEV), V.to(DEV), cu.to(DEV)))
+    solo = [ra._tree_forward(*s, b, d, N, False, _lib.ALGO_SUBTREE)[0].clone() for s in sets]
     torch.cuda.synchronize()
-    for k, o in outs:
-        assert torch.equal(o, solo[k]), f"set {k}"
+    before = _lib.sched_info()
+    graphs, outs = [], []
+    for gi in range(ngraphs):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            og = [ra._tree_forward(*sets[(gi + r) % nsets], b, d, N, False, _lib.ALGO_SUBTREE)[0]
+                  for r in range(per_graph)]
+        graphs.append(g)
+        outs.append(og)
+    mid = _lib.sched_info()
+    say("sched_info", before, mid)
+    assert mid["static_launches"] == before["static_launches"]
+    assert mid["dynamic_launches"] - before["dynamic_launches"] == ngraphs * per_graph
+    assert mid["capture_slots"] - before["capture_slots"] == ngraphs
+    for rep in range(3):
+        for g in graphs:
+            g.replay()
+        torch.cuda.synchronize()
+        for gi, og in enumerate(outs):
+            for r, o in enumerate(og):
+                assert torch.equal(o, solo[(gi + r) % nsets]), f"replay {rep} graph {gi} launch {r}"
+    del graphs, outs, og, g
+    gc.collect()
+    torch.cuda.synchronize()
+
+    def held():
+        return _lib.sched_info()["capture_slots"]
+
+    t0 = time.time()
+    while held() > before["capture_slots"] and time.time() - t0 < 5.0:
+        time.sleep(0.01)
+    assert held() == before["capture_slots"], _lib.sched_info()
+    # churn: more captures than slots, each graph destroyed after one replay
+    for gi in range(200):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            o = ra._tree_forward(*sets[gi % nsets], b, d, N, False, _lib.ALGO_SUBTREE)[0]
+        g.replay()
+        torch.cuda.synchronize()
+        if gi % 50 == 0:
+            assert torch.equal(o, solo[gi % nsets]), f"churn graph {gi}"
+        del g, o
+        gc.collect()
+    torch.cuda.synchronize()
+    end = _lib.sched_info()
+    say("sched_info after churn", end)
+    assert end["static_launches"] == before["static_launches"]
 
 
 def test_graph_replays_and_eager_launches_interleaved():

@@ -1,12 +1,17 @@
 """The reference's correctness sweep on the HIP path, every output checked.
 
 Configurations follow scripts/correctness_benchmark.py:287-315 of the
-reference (deduplicated in the order its main() uses, :344-350):
+reference (its full run, deduplicated in the order its main() uses,
+:350-356: 104 configurations):
 
-  standard  (B, b, d, 4, 64) for (B, b, d) in (1,2,3), (4,3,5), (2,4,5)  (:287-292)
-  LLaMA     B in {1,2,4} x b in {2,3,4} x d in {3,5,7} at H=32, D=128   (:298-305)
+  standard  B in {1,2,4,8} x b in {1,2,3} x d in {1..6} at H=4, D=64  (:287-294)
+  LLaMA     B in {1,2,4} x b in {2,3,4} x d in {3,5,7} at H=32, D=128 (:297-304)
   edge      (4,1,0,4,64) (4,1,8,4,64) (4,2,8,4,64) (2,4,5,32,128)
-            (8,4,5,32,128) (4,2,3,4,32)                                (:308-315)
+            (8,4,5,32,128) (4,2,3,4,32)                              (:307-314)
+
+The reference's --fast subset, (1,2,3) (4,3,5) (2,4,5) at (4,64) and
+(32,128) (:316-320), adds one configuration outside the full run,
+(2,4,5,4,64), which runs here as well.
 
 Inputs are drawn as the reference draws them (:183-195): fp16 randn on the
 device, seed B*10000 + b*1000 + d*100 + H*10 + D, all Q then all K then all V
@@ -33,10 +38,11 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda"
 FP16_TOL = 2e-3
 
-_STANDARD = [(B, b, d, 4, 64) for B, b, d in [(1, 2, 3), (4, 3, 5), (2, 4, 5)]]
+_STANDARD = [(B, b, d, 4, 64) for B in (1, 2, 4, 8) for b in (1, 2, 3) for d in range(1, 7)]
 _LLAMA = [(B, b, d, 32, 128) for B in (1, 2, 4) for b in (2, 3, 4) for d in (3, 5, 7)]
 _EDGE = [(4, 1, 0, 4, 64), (4, 1, 8, 4, 64), (4, 2, 8, 4, 64), (2, 4, 5, 32, 128),
          (8, 4, 5, 32, 128), (4, 2, 3, 4, 32)]
+_FAST = [(B, b, d, H, D) for B, b, d in [(1, 2, 3), (4, 3, 5), (2, 4, 5)] for H, D in [(4, 64), (32, 128)]]
 
 
 def _sweep():
@@ -49,14 +55,18 @@ def _sweep():
 
 
 SWEEP = _sweep()
+FAST_EXTRA = [c for c in _FAST if c not in SWEEP]
 
 
 def test_sweep_size():
-    """35 distinct configurations, as the reference's full run prints."""
-    assert len(SWEEP) == 35
+    """104 distinct configurations, as the reference's full run prints
+    (72 standard + 27 LLaMA + 5 edge cases not already listed); the --fast
+    subset adds (2,4,5,4,64)."""
+    assert len(SWEEP) == 104
+    assert FAST_EXTRA == [(2, 4, 5, 4, 64)]
 
 
-@pytest.mark.parametrize("B,b,d,H,D", SWEEP)
+@pytest.mark.parametrize("B,b,d,H,D", SWEEP + FAST_EXTRA)
 def test_reference_sweep(B, b, d, H, D):
     from qattention_amd import ragged_attn as ra
 

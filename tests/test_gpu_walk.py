@@ -229,17 +229,144 @@ def test_prefix_parents_walk_bitexact(ns):
     _check_out(O, o_ref, "prefix parents outputs")
 
 
-def test_walk_export_rejects_unsupported_calls():
-    """The export covers fp16 calls over packed cu_seqlens without LSE; other
-    calls fail loudly while it is on, and it is off again afterwards."""
+# (dtype, with LSE): the instantiations that serve bf16 calls and the
+# LSE-returning calls (ragged_attention_with_lse, return_lse=True prefix calls)
+VARIANTS = [(torch.bfloat16, False), (torch.float16, True), (torch.bfloat16, True)]
+
+
+def _check_out_dt(O, o_ref, dtype, what):
+    """fp16: max abs <= 2e-3; bf16: half an ulp of max(1, |o|) (2^-8) plus the
+    prefix path's P rounding, 2^-7 max(1, |o|) + 1e-3."""
+    o = O.double().cpu().numpy()
+    if dtype == torch.float16:
+        _check_out(O, o_ref, what)
+    else:
+        bound = 2.0 ** -7 * np.maximum(1.0, np.abs(o_ref)) + 1e-3
+        assert (np.abs(o - o_ref) <= bound).all(), f"{what}: bf16 err {np.abs(o - o_ref).max():.3e}"
+
+
+def _check_lse(LSE, lse_ref, dtype, what):
+    err = float(np.abs(LSE.double().cpu().numpy() - lse_ref).max()) if LSE.numel() else 0.0
+    assert err <= (1e-4 if dtype == torch.float16 else 2e-3), f"{what}: LSE err {err:.3e}"
+
+
+@pytest.mark.parametrize("dtype,lse", VARIANTS)
+@pytest.mark.parametrize("lens,b,md,Hq,Hkv,D", [([1365] * 4, 4, 5, 32, 32, 128),   # cfg2
+                                               ([4681] * 2, 8, 4, 32, 32, 128),   # cfg5's tree
+                                               ([13, 0, 40, 1, 7], 3, 3, 8, 2, 64)])
+@pytest.mark.parametrize("algo", ["subtree", "gather"])
+def test_heap_walk_bitexact_bf16_lse(lens, b, md, Hq, Hkv, D, algo, dtype, lse):
     ra, _lib = _mods()
-    Q, K, V, cu = make_inputs([15, 15], 4, 64, 4500)
-    Qd, Kd, Vd = Q.to(DEV), K.to(DEV), V.to(DEV)
-    table = _table(30, 4, 3)
+    say("walk heap", algo, dtype, "lse" if lse else "", lens[:3], b, md, Hq, Hkv, D)
+    code = _lib.ALGO_SUBTREE if algo == "subtree" else _lib.ALGO_GATHER
+    Q, K, V, cu = make_inputs(lens, Hq, D, 4600 + b * 10 + md, dtype=dtype, Hkv=Hkv)
+    T = Q.shape[0]
+    table = _table(T, Hq, md)
+    with _lib.debug_walk(table):
+        O, LSE = ra._tree_forward(Q.to(DEV), K.to(DEV), V.to(DEV), cu, b, md, None, lse, code)
+    torch.cuda.synchronize()
+    _expect(table, clib.ancestor_table_heap(cu.numpy(), b, md), f"{algo} {dtype} walk")
+    if T * Hq <= 400_000:
+        o_ref, lse_ref, _ = oracle_tree(Q, K, V, cu, b, md)
+        _check_out_dt(O, o_ref, dtype, f"{algo} outputs")
+        if lse:
+            _check_lse(LSE, lse_ref, dtype, algo)
+
+
+@pytest.mark.parametrize("dtype,lse", VARIANTS)
+@pytest.mark.parametrize("algo", ["subtree", "gather"])
+def test_paged_walk_bitexact_bf16_lse(algo, dtype, lse):
+    ra, _lib = _mods()
+    lens, b, md, H, D = [1365, 341], 4, 5, 8, 128
+    say("walk paged", algo, dtype, lse)
+    code = _lib.ALGO_SUBTREE if algo == "subtree" else _lib.ALGO_GATHER
+    Q, K, V, cu = make_inputs(lens, H, D, 4700, dtype=dtype)
+    Kc, Vc, pt = ra.build_paged_kv([K[:1365], K[1365:]], [V[:1365], V[1365:]], 16)
+    perm = torch.randperm(Kc.shape[0], generator=torch.Generator().manual_seed(4701))
+    Kp, Vp = torch.empty_like(Kc), torch.empty_like(Vc)
+    Kp[perm], Vp[perm] = Kc, Vc
+    ptp = perm.to(torch.int32)[pt.long()]
+    T = Q.shape[0]
+    table = _table(T, H, md)
+    with _lib.debug_walk(table):
+        O, LSE = ra._paged_forward(Q.to(DEV), Kp.to(DEV), Vp.to(DEV), ptp, cu, b, md, None, lse, code)
+    torch.cuda.synchronize()
+    _expect(table, clib.ancestor_table_heap(cu.numpy(), b, md), f"{algo} paged walk")
+    o_ref, lse_ref, _ = oracle_tree(Q, K, V, cu, b, md)
+    _check_out_dt(O, o_ref, dtype, f"{algo} paged outputs")
+    if lse:
+        _check_lse(LSE, lse_ref, dtype, f"{algo} paged")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_parents_walk_bitexact_bf16_lse(dtype):
+    """ragged_attention_with_parents returns LSE: the LSE instantiations of
+    the parents walk, in both dtypes."""
+    ra, _lib = _mods()
+    lens, md, Hq, D = [60, 0, 1024], 7, 8, 128
+    say("walk parents", dtype)
+    Q, K, V, cu = make_inputs(lens, Hq, D, 4800, dtype=dtype)
+    par = _random_parents(lens, 4801, 10)
+    T = Q.shape[0]
+    table = _table(T, Hq, md)
+    with _lib.debug_walk(table):
+        O, LSE = ra.ragged_attention_with_parents(Q.to(DEV), K.to(DEV), V.to(DEV), cu, torch.from_numpy(par), md)
+    torch.cuda.synchronize()
+    _expect(table, clib.ancestor_table_parents(cu.numpy(), par, md), "parents walk")
+    o_ref, lse_ref, _ = oracle_tree(Q, K, V, cu, 2, md, parents=par)
+    _check_out_dt(O, o_ref, dtype, "parents outputs")
+    _check_lse(LSE, lse_ref, dtype, "parents")
+
+
+# prefix calls: cfg5 (one split, the fused epilogue's staged walk), cfg4
+# (five splits merged by the gather walk, and forced into one split), and
+# several splits merged by the subtree kernel
+PREFIX_VARIANT_CASES = [
+    ([4681] * 16, 8, 4, 32, 32, 2048, 0),
+    ([85] * 4, 4, 3, 32, 8, 10240, 0),
+    ([85] * 4, 4, 3, 32, 8, 10240, 1),
+    ([1365] * 4, 4, 5, 32, 32, 256, 4),
+]
+
+
+@pytest.mark.parametrize("dtype,lse", VARIANTS)
+@pytest.mark.parametrize("lens,b,md,Hq,Hkv,L,ns", PREFIX_VARIANT_CASES)
+def test_prefix_walk_bitexact_bf16_lse(lens, b, md, Hq, Hkv, L, ns, dtype, lse):
+    ra, _lib = _mods()
+    say("walk prefix", dtype, lse, lens[:3], b, md, Hq, Hkv, L, ns)
+    D = 128
+    Q, K, V, cu = make_inputs(lens, Hq, D, 4900 + b * 10 + md, dtype=dtype, Hkv=Hkv)
+    g = torch.Generator().manual_seed(4901 + L)
+    Kp = torch.randn(len(lens), L, Hkv, D, generator=g).to(dtype)
+    Vp = torch.randn(len(lens), L, Hkv, D, generator=g).to(dtype)
+    T = Q.shape[0]
+    table = _table(T, Hq, md)
+    with _lib.debug_walk(table):
+        out = ra.ragged_attention_prefix(Q.to(DEV), K.to(DEV), V.to(DEV), cu, Kp.to(DEV), Vp.to(DEV), b, md,
+                                         num_splits=ns, return_lse=lse)
+    torch.cuda.synchronize()
+    O, LSE = out if lse else (out, None)
+    _expect(table, clib.ancestor_table_heap(cu.numpy(), b, md), f"prefix walk {dtype}")
+    if T * Hq * L <= 50_000_000:
+        o_ref, lse_ref, _ = oracle_tree(Q, K, V, cu, b, md, Kp=Kp, Vp=Vp)
+        _check_out_dt(O, o_ref, dtype, "prefix outputs")
+        if lse:
+            _check_lse(LSE, lse_ref, dtype, "prefix")
+
+
+def test_walk_export_rejects_unsupported_calls():
+    """The export covers calls over packed cu_seqlens (either dtype, with or
+    without LSE); the uniform-batch [B, H, N, D] call fails loudly while it
+    is on, and the export is off again afterwards."""
+    ra, _lib = _mods()
+    B, N, H, D = 2, 15, 4, 64
+    Q, K, V, cu = make_inputs([N] * B, H, D, 4500)
+    q4 = Q.view(B, N, H, D).permute(0, 2, 1, 3).to(DEV)
+    k4 = K.view(B, N, H, D).permute(0, 2, 1, 3).to(DEV)
+    v4 = V.view(B, N, H, D).permute(0, 2, 1, 3).to(DEV)
+    table = _table(B * N, H, 3)
     with _lib.debug_walk(table):
         with pytest.raises(_lib.QAttnError):
-            ra.ragged_attention_with_lse(Qd, Kd, Vd, cu, 2, 3)
-        with pytest.raises(_lib.QAttnError):
-            ra.ragged_attention(Qd.bfloat16(), Kd.bfloat16(), Vd.bfloat16(), cu, 2, 3)
-    O, L = ra.ragged_attention_with_lse(Qd, Kd, Vd, cu, 2, 3)  # export off: works
-    assert torch.isfinite(O.float()).all()
+            ra.ragged_tree_attn(q4, k4, v4, 2, 3)
+    O4 = ra.ragged_tree_attn(q4, k4, v4, 2, 3)  # export off: works
+    assert torch.isfinite(O4.float()).all()
