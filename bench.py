@@ -1,8 +1,9 @@
 """Benchmark of the tree-verify attention hot path on one MI355X.
 
     python bench.py [--steps K] [--warmup W] [--config cfg2|cfg3|cfg4|cfg4_prefix|cfg5|gen1024|cfg4_bhnd|cfg2_paged|eagle3|merge4
-                    |cfg2_bf16|cfg4_bf16|cfg4_shared]
+                    |cfg2_bf16|cfg4_bf16|cfg4_shared|micro28_B1|micro28_B4|micro28_B8|micro28_B8_L4096]
                     [--algo auto|gather|subtree] [--no-extra] [--no-cpu-baseline]
+    python bench.py --config cfg4 --eager-calls 4     (counter passes: N eager calls, no graphs)
 
 A step is one full verify-attention call (all sequences, all heads, and the
 prefix KV cache when the config has one) over one batch of synthetic input,
@@ -31,7 +32,11 @@ Prints ONE JSON line with the driver's fields plus
                 kernel reaches under the same cache conditions
   extra         (default cfg2 run) cfg3, the cfg4 verify call, the cfg4
                 prefix-only call (same queries and prefix, no tree keys) and
-                their ratio, each timed the same way
+                their ratio, cfg5, one EAGLE-3 step and the reference's
+                published balanced micro-benchmark shapes, each timed the
+                same way
+  sched_static_launches  subtree launches of the run that fell back to the
+                static schedule for want of a counter slot (expected 0)
   cpu_baseline  the reference's CPU path (padded SDPA + tree mask, fp32, MATH
                 backend; restated in oracle/sdpa.py) timed on this host's cores
 """
@@ -89,7 +94,21 @@ CONFIGS = {
     # sequence's prefix for all four), as the reference's micro-benchmark
     # shares K_sh/V_sh across its branches (scripts/benchmark_micro.py:318-331)
     "cfg4_shared": dict(B=4, b=4, d=3, H=32, Hkv=8, D=128, L=10240, sigma=1.0, layout="shared_prefix"),
+    # The reference's published kernel rows for this path, its balanced
+    # micro-benchmark (scripts/benchmark_micro.py --balanced-trees, budgeted
+    # N): a b=28 heap tree capped at N=672 nodes (depth 2, max_depth 2),
+    # H=32, D=128, fp16, B = 1, 4, 8 (results/balanced_micro/aggregate.csv:
+    # 17, 81, 113: 22.3, 272.9, 553.1 us), and B=8 over a 4096-token prefix
+    # shared by the batch (:129, 6454.2 us; scripts/benchmark_micro.py:
+    # 568-593: shared-prefix pass + tree pass + fused_lse_merge), other hardware
+    "micro28_B1": dict(B=1, b=28, d=2, H=32, Hkv=32, D=128, L=0, sigma=1.0, N=672),
+    "micro28_B4": dict(B=4, b=28, d=2, H=32, Hkv=32, D=128, L=0, sigma=1.0, N=672),
+    "micro28_B8": dict(B=8, b=28, d=2, H=32, Hkv=32, D=128, L=0, sigma=1.0, N=672),
+    "micro28_B8_L4096": dict(B=8, b=28, d=2, H=32, Hkv=32, D=128, L=4096, sigma=1.0, N=672,
+                             layout="shared_prefix"),
 }
+# the reference's published time for each micro config (us per call, other hardware)
+PUBLISHED_US = {"micro28_B1": 22.3, "micro28_B4": 272.9, "micro28_B8": 553.1, "micro28_B8_L4096": 6454.2}
 
 
 def torch_dtype(c):
@@ -458,6 +477,21 @@ def hbm_ceiling(alg_bytes, steps, warmup):
             "frac": round(alg_bytes / (us * 1e-6) / PEAK_HBM, 4)}
 
 
+def eager_calls(name, algo, n, forced_sets=0):
+    """n eager calls of a config on rotating input sets (call k reads set k
+    mod nsets, as in the timed runs), synchronised at the end: the workload a
+    rocprofv3 --pmc counter pass collects from, one dispatch group per call."""
+    import torch
+    call, nsets = build_workload(name, algo, forced_sets)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for k in range(n):
+        call(k % nsets)
+    torch.cuda.synchronize()
+    print(json.dumps({"eager_calls": n, "config": name, "sets": nsets,
+                      "wall_us_per_call": round((time.perf_counter() - t0) / n * 1e6, 2)}), flush=True)
+
+
 def measure(name, algo, steps, warmup, forced_sets=0):
     """(µs per call from events, µs per call of wall time, input sets)."""
     import torch
@@ -481,6 +515,9 @@ def main():
     ap.add_argument("--sets", type=int, default=0, help="rotating input sets (0: see n_sets)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain MIB-MiB device copy (counter calibration) and exit")
+    ap.add_argument("--eager-calls", type=int, default=0, metavar="N",
+                    help="only run N eager calls of --config on rotating input sets (no graphs, no "
+                         "timing) and exit: the workload of a rocprofv3 --pmc counter pass")
     args = ap.parse_args()
     if args.copy_calibration:
         copy_calibration(args.copy_calibration)
@@ -499,6 +536,9 @@ def main():
 
     torch.cuda.set_device(torch.device("cuda:0"))
     algo = {"auto": _lib.ALGO_AUTO, "gather": _lib.ALGO_GATHER, "subtree": _lib.ALGO_SUBTREE}[args.algo]
+    if args.eager_calls:
+        eager_calls(args.config, algo, args.eager_calls, args.sets)
+        return
     c = CONFIGS[args.config]
     B, b, d, H, Hkv, D, L = (c[k] for k in ("B", "b", "d", "H", "Hkv", "D", "L"))
     N = tree_size(c)
@@ -528,6 +568,18 @@ def main():
         # one EAGLE-3 verify step (latency-bound: a decode step of a small draft tree)
         use3, _, _ = measure("eagle3", _lib.ALGO_AUTO, args.steps, args.warmup)
         extra.update({"eagle3_us": round(use3, 2)})
+        # cfg5: the MFMA prefix (L=2048) and a 74,896-token tree walk in one call
+        us5, _, _ = measure("cfg5", _lib.ALGO_AUTO, args.steps, args.warmup)
+        r5 = roofline_of(CONFIGS["cfg5"], us5)
+        extra.update({"cfg5_us": round(us5, 2), "cfg5_frac": r5["frac"], "cfg5_mfma_frac": r5["mfma_frac"],
+                      "cfg5_hbm_frac": r5["hbm_frac"]})
+        # the reference's published balanced micro-benchmark rows (other hardware)
+        micro = {}
+        for name in ("micro28_B1", "micro28_B4", "micro28_B8", "micro28_B8_L4096"):
+            usm, _, _ = measure(name, _lib.ALGO_AUTO, args.steps, args.warmup)
+            micro[name] = {"us": round(usm, 2), "frac": roofline_of(CONFIGS[name], usm)["frac"],
+                           "reference_us": PUBLISHED_US[name]}
+        extra["micro28"] = micro
 
     cpu = None
     if not args.no_cpu_baseline and layout not in ("merge", "prefix_only"):
@@ -564,6 +616,7 @@ def main():
         "hbm_ceiling": ceiling,
         "extra": extra,
         "cpu_baseline": cpu,
+        "sched_static_launches": _lib.sched_info()["static_launches"],
     }
     print(json.dumps(out), flush=True)
 
