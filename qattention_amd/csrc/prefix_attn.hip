@@ -66,6 +66,15 @@ __device__ __forceinline__ int kv_swz(int r, int dv) {
     return ((2 * (r & 3)) | (8 * (b3 ^ b2)) | b2) & (dv - 1);
 }
 
+// Chunk swizzle of the K/V blocks of the 32x32x16 prefix kernel: chunk c of
+// key row r sits at c ^ kv_swz32(r).  Its K operand reads (ds_read_b128, 16
+// consecutive rows at one chunk per 16-lane pass) need 16 distinct positions
+// for rows r..r+15, which a bijection on r & 15 gives; its V^T operand reads
+// (ds_read_b64_tr_b16, per 32-lane pass 4 consecutive rows x one aligned
+// group of 4 chunks) need the 4 rows in distinct groups, which 4 (r & 3)
+// gives.  (Positions checked on the CPU for every pass at D = 128.)
+__device__ __forceinline__ int kv_swz32(int r, int dv) { return ((4 * (r & 3)) | ((r >> 2) & 3)) & (dv - 1); }
+
 // s_waitcnt immediate (gfx9 encoding): vmcnt N, expcnt and lgkmcnt unconstrained
 constexpr int kWaitVm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 
@@ -96,16 +105,561 @@ __device__ __forceinline__ void lds_dma16(uint32_t voff, const char* sbase, void
     asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(lds) : "memory");
 }
 
+// The prefix kernel: 128-row query tiles, each wave owning 32 rows as the N
+// dimension of v_mfma_f32_32x32x16 products.  Per 64-key block a wave runs
+//   S^T = K Q^T      2 key tiles x D/16 k-steps   (A: K rows from LDS, B: Q in registers)
+//   O^T += V^T P^T   4 16-key steps x D/32 d-tiles (A: V^T from LDS, B: P^T in registers)
+// Lane l holds query l % 32; lanes l and l + 32 split the query's keys (S^T)
+// and head dims (O^T), so the softmax statistics need one xor-32 exchange.
+// The S^T output registers are the P^T operand: PV step (t, h) takes
+// elements 8h .. 8h+7 of S tile t, i.e. keys 32t + 16h + {0..3, 8..11} on
+// lanes 0-31 and + {4..7, 12..15} on lanes 32-63, and the V^T operand is
+// read in that key order.
 // WALK: the tree walk of the fused epilogue (heap or explicit parents, or
 // none for the prefix-only pass); the split kernels leave the walk to the tree
 // kernels.  DBG: the walk-export instantiation (qattn_debug_walk), which also
 // writes each query's attended ancestors to tp.dbg_walk.
-// QB: 16-row column blocks per wave (2; 1 halves the query tile for calls
-// whose split units would leave CUs idle, split kernels only).
-template <typename T, int D, bool FUSED, bool LSE, int WALK, bool BATCH, bool DBG = false, int QB = 2>
+template <typename T, int D, bool FUSED, bool LSE, int WALK, bool BATCH, bool DBG = false>
 __global__ __launch_bounds__(kPrefixThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefix_attn_kernel(
     PrefixParams p, TreeParams tp) {
-    static_assert(QB == 2 || (QB == 1 && !FUSED), "the fused epilogue walks two column blocks per wave");
+    constexpr int kQB = 2;          // 16-row column blocks per wave (the epilogue's walk layout)
+    constexpr int kBM = 128;        // query rows per workgroup
+    constexpr int KS = D / 16;      // k-steps of S^T over the head dim
+    constexpr int DT = D / 32;      // 32-row d-tiles of O^T
+    constexpr int DV = D / 8;       // 16-byte chunks per key row
+    constexpr int BLK = kBN * D;    // elements of one K or V block
+    constexpr int NI = D / 32;      // 1 KB LDS loads per thread per K (or V) block
+    constexpr int RPI = 512 / D;    // key rows per 1 KB load
+    static_assert(NI * 4 * 512 == BLK, "a block is 4 waves x NI loads of 1 KB");
+    // Double buffers of the K and V blocks, four LDS variables so that the
+    // compiler tells them apart: a read of one buffer does not wait for the
+    // LDS-DMA loads in flight into another.
+    __shared__ __attribute__((aligned(1024))) uint16_t Kb0[BLK], Kb1[BLK], Vb0[BLK], Vb1[BLK];
+    // DBG only: the node of each row the epilogue stages in LDS
+    __shared__ int32_t dbg_slot[DBG ? 2 * (BLK / D) : 1];
+    auto kbuf = [&](auto i) -> uint16_t* {
+        if constexpr (decltype(i)::value == 0) return Kb0; else return Kb1;
+    };
+    auto vbuf = [&](auto i) -> uint16_t* {
+        if constexpr (decltype(i)::value == 0) return Vb0; else return Vb1;
+    };
+
+    // Logical unit order puts the query tiles of one (sequence, kv head, split)
+    // next to each other; hardware deals blockIdx round-robin over the 8 XCDs,
+    // so unit u runs on XCD (blockIdx % 8) and a K/V block is shared in one L2.
+    const int per = gridDim.x >> 3;
+    const int unit = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
+    if (unit >= p.n_units) return;
+    // (magic-number divisions: the generic 32-bit ones held the first loads
+    // of a short launch back)
+    const int r0 = divide(unit, p.qtdiv);
+    const int qt = unit - r0 * p.qtiles;
+    const int r1 = divide(r0, p.nsdiv);
+    const int split = r0 - r1 * p.n_split;
+    const int seq = divide(r1, p.hkvdiv);
+    const int kvh = r1 - seq * p.Hkv;
+
+    // (BATCH: a uniform batch of max_seqlen rows per sequence, no cu)
+    const int32_t s0 = BATCH ? seq * p.max_seqlen : p.cu[seq];
+    const int32_t s1 = BATCH ? s0 + p.max_seqlen : p.cu[seq + 1];
+    if (s0 < 0 || s1 < s0 || (int64_t)s1 > p.total_tokens) return;
+    int32_t n = s1 - s0;
+    if (n > p.max_seqlen) n = p.max_seqlen;
+    const int g = p.group;
+    const int rows = n * g;
+    if (qt * kBM >= rows) return;
+
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lane = tid & 63;
+    const int q32 = lane & 31, hl = lane >> 5;
+
+    // this lane's query row (B operand column, output column), recomputed
+    // after the key loop rather than kept live through it
+    auto query_of = [&](int64_t& qrow, int& qh) {
+        const int rr = qt * kBM + wave * 32 + q32;
+        const int tok = divide(rr, p.gdiv);
+        qh = kvh * g + (rr - tok * g);
+        qrow = (int64_t)s0 + tok;
+        return rr < rows;
+    };
+    // Q^T operand of step s: dims 16 s + 8 hl .. + 7 of the lane's query
+    Vec16 qf[KS];
+    {
+        int64_t qrow;
+        int qh;
+        const bool valid = query_of(qrow, qh);
+        const uint16_t* qp = (const uint16_t*)p.q + qrow * p.sq_t + (BATCH ? (int64_t)seq * p.sq_b : 0) +
+                             (int64_t)qh * p.sq_h + 8 * hl;
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+            qf[s] = Vec16{{0u, 0u, 0u, 0u}};
+            if (valid) qf[s] = ld16(qp + 16 * s);
+        }
+    }
+
+    const int k_lo = split * p.blocks_per_split * kBN;
+    const int k_hi = (k_lo + p.blocks_per_split * kBN < p.L) ? k_lo + p.blocks_per_split * kBN : p.L;
+    const int nb = (k_hi - k_lo + kBN - 1) / kBN;  // >= 1: every split holds a key
+    const char* kbase = (const char*)((const uint16_t*)p.kp + (int64_t)seq * p.skp_b + (int64_t)kvh * p.skp_h);
+    const char* vbase = (const char*)((const uint16_t*)p.vp + (int64_t)seq * p.svp_b + (int64_t)kvh * p.svp_h);
+    const int64_t kst = 2 * p.skp_t, vst = 2 * p.svp_t;  // bytes between keys
+
+    float m_run = -INFINITY, l_run = 0.f;  // l_run: this lane's half of the keys
+    f16v_t oacc[DT];
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) oacc[dt][r] = 0.f;
+
+    // ---- K/V blocks go straight from global memory to LDS (global_load_lds,
+    // 16 bytes per lane, lane i of a load writes bytes [16 i, 16 i + 16) of its
+    // 1 KB): load i of wave w covers key rows (w NI + i) RPI .. + RPI - 1, and
+    // each lane fetches the chunk that the swizzle puts at its position ----
+    // Byte offsets of this lane's loads within a block: 32-bit (the host checks
+    // that 64 key rows span less than 4 GB), added to the block's uniform base.
+    uint32_t koff[NI], voff[NI];
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+        const int row = (wave * NI + i) * RPI + lane / DV;
+        const uint32_t col = 16 * ((lane % DV) ^ kv_swz32(row, DV));
+        koff[i] = (uint32_t)row * (uint32_t)kst + col;
+        voff[i] = (uint32_t)row * (uint32_t)vst + col;
+    }
+    auto issue = [&](const char* base, int64_t st, const uint32_t (&off)[NI], int j, uint16_t* buf) {
+        const int kb = k_lo + j * kBN;
+        const char* gb = base + (int64_t)kb * st;
+        if (__builtin_expect(kb + kBN <= k_hi, 1)) {
+#pragma unroll
+            for (int i = 0; i < NI; ++i) lds_dma16(off[i], gb, buf + (wave * NI + i) * 512);
+        } else {
+            // tail block of the split: rows past k_hi - 1 load that key instead
+            const int last = k_hi - 1 - kb;
+#pragma unroll
+            for (int i = 0; i < NI; ++i) {
+                const int row = (wave * NI + i) * RPI + lane / DV;
+                const uint32_t col = 16 * ((lane % DV) ^ kv_swz32(row, DV));
+                lds_dma16((uint32_t)min(row, last) * (uint32_t)st + col, gb, buf + (wave * NI + i) * 512);
+            }
+        }
+    };
+    auto issue_k = [&](int j, auto buf) { issue(kbase, kst, koff, j, kbuf(buf)); };
+    auto issue_v = [&](int j, auto buf) { issue(vbase, vst, voff, j, vbuf(buf)); };
+
+    // Operand read addresses (elements).  K (A of S^T, step s, key tile t):
+    // row 32 t + q32, chunk 2 s + hl: (kaddr0 ^ 16 s) + 32 D t (the swizzle
+    // flips only chunk bits, which the row base leaves clear).  V^T (A of
+    // O^T, 16-key step th = 2t + h, d-tile dt): two ds_read_b64_tr_b16, X for
+    // keys 16 th + 4 hl + 0..3 and Y for + 8; within each 16-lane group lane
+    // j points at row key0 + j / 4, dims 32 dt + 16 ((lane >> 4) & 1) +
+    // 4 (j % 4) .. + 3, and receives keys key0 + 0..3 at dim 32 dt + q32.
+    const int kaddr0 = q32 * D + 8 * (hl ^ kv_swz32(q32, DV));
+    int vx0, vy0;
+    {
+        const int rx = 4 * hl + ((lane & 15) >> 2), ry = rx + 8;
+        const int cx = 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
+        vx0 = rx * D + 8 * (cx ^ kv_swz32(rx, DV)) + 4 * (lane & 1);
+        vy0 = ry * D + 8 * (cx ^ kv_swz32(ry, DV)) + 4 * (lane & 1);
+    }
+
+    // S^T = K Q^T of the block in K buffer buf; step i = (k-step i / 2, key
+    // tile i % 2), so consecutive products write different tiles, and the K
+    // operand of step i + 1 is read before the product of step i is issued.
+    auto s_product = [&](auto buf, f16v_t (&s)[2]) {
+        const uint16_t* kb = kbuf(buf);
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) s[t][r] = 0.f;
+        constexpr int NS = 2 * KS;
+        auto fetch = [&](int i) { return ld16(kb + (kaddr0 ^ (16 * (i >> 1))) + 32 * D * (i & 1)); };
+        Vec16 ka[3];
+        ka[0] = fetch(0);
+        ka[1] = fetch(1);
+#pragma unroll
+        for (int i = 0; i < NS; ++i) {
+            if (i + 2 < NS) ka[(i + 2) % 3] = fetch(i + 2);
+            s[i & 1] = mma32<T>(ka[i % 3], qf[i >> 1], s[i & 1]);
+        }
+    };
+
+    // Online softmax of one block (the lane's query; keys 32 t + 8 (r / 4) +
+    // 4 hl + r % 4 of element r of tile t).  The running max is kept on raw
+    // scores q.k (scale > 0 keeps the order) and scale*log2(e) is folded into
+    // the exponent: p = exp2(s c - m c), one FMA.  Lazy rescaling: the
+    // exponent reference m_run only moves when a block max exceeds it by more
+    // than kLazy/c (a factor 2^kLazy in P), so the accumulators are rescaled on
+    // a handful of blocks.  P stays <= 2^kLazy and l carries the same
+    // reference.  The PV product rounds P to the input type while l sums it
+    // unrounded, so the largest weight is exact only when it is 1: bf16 (8
+    // mantissa bits) therefore moves the reference on every new maximum, as
+    // the reference's FA2 loop does; fp16 (11 bits) keeps the lazy reference.
+    const float csc = p.scale_log2;
+    auto softmax = [&](f16v_t (&s)[2], Vec16 (&pf)[4], float& alpha, bool& rescale, int kb, auto mask_tag) {
+        constexpr bool MASK = decltype(mask_tag)::value;
+        constexpr float kLazy = T::kCode == QATTN_DTYPE_BF16 ? 0.f : 8.f;
+        if constexpr (MASK) {  // tail block of the split: keys at or beyond k_hi do not exist
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    if (kb + 32 * t + 8 * (r >> 2) + 4 * hl + (r & 3) >= k_hi) s[t][r] = -INFINITY;
+        }
+        float mb = -INFINITY;
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) mb = fmaxf(mb, s[t][r]);
+        mb = xor32_max(mb);
+        const bool move = (mb - m_run) * csc > kLazy;  // always true on the first block
+        const float m_new = move ? mb : m_run;
+        alpha = move ? fast_exp2((m_run - m_new) * csc) : 1.f;  // m_run = -inf: 0
+        rescale |= move;
+        const float mc = m_new * csc;
+        float psum = 0.f;
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const float e = fast_exp2(__builtin_fmaf(s[t][r], csc, -mc));
+                s[t][r] = e;
+                psum += e;
+            }
+        }
+        l_run = l_run * alpha + psum;
+        m_run = m_new;
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    pf[2 * t + h].w[i] = MfmaOps<T>::pack2(s[t][8 * h + 2 * i], s[t][8 * h + 2 * i + 1]);
+    };
+    auto rescale_o = [&](float alpha, bool rescale) {
+        // the accumulators need rescaling only when some running max moved
+        if (__builtin_expect(__any(rescale), 0)) {
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) oacc[dt] *= alpha;
+        }
+    };
+
+    // O^T += V^T P^T of the block in V buffer buf; step i = (16-key step
+    // i / DT, d-tile i % DT), operands read one step ahead
+    auto pv_product = [&](auto buf, const Vec16 (&pf)[4]) {
+        typedef short v4s __attribute__((ext_vector_type(4)));
+        const uint16_t* vb = vbuf(buf);
+        auto fetch = [&](int i) {
+            const int th = i / DT, dt = i % DT;
+            const uint16_t* ax = vb + (vx0 ^ (32 * dt)) + 16 * D * th;
+            const uint16_t* ay = vb + (vy0 ^ (32 * dt)) + 16 * D * th;
+            const v4s x = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s*)ax);
+            const v4s y = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s*)ay);
+            const uint2 x2 = __builtin_bit_cast(uint2, x), y2 = __builtin_bit_cast(uint2, y);
+            return Vec16{{x2.x, x2.y, y2.x, y2.y}};
+        };
+        constexpr int NS = 4 * DT;
+        Vec16 va[3];
+        va[0] = fetch(0);
+        if (NS > 1) va[1] = fetch(1);
+#pragma unroll
+        for (int i = 0; i < NS; ++i) {
+            if (i + 2 < NS) va[(i + 2) % 3] = fetch(i + 2);
+            oacc[i % DT] = mma32<T>(va[i % 3], pf[i / DT], oacc[i % DT]);
+        }
+    };
+
+    // ---- pipeline over the split's blocks j = 0 .. nb-1: iteration j starts
+    // after a barrier that publishes K_{j+1} and V_j, issues V_{j+1} and
+    // K_{j+2} into the buffers freed by the barrier, forms S_{j+1} on the
+    // matrix cores while the softmax of block j runs on the vector ALUs, and
+    // ends with the PV product of block j ----
+    using B0 = std::integral_constant<int, 0>;
+    using B1 = std::integral_constant<int, 1>;
+    issue_k(0, B0{});
+    issue_v(0, B0{});
+    if (nb > 1) {
+        issue_k(1, B1{});
+        __builtin_amdgcn_s_waitcnt(kWaitVm(NI));  // K_0 and V_0 (and Q) have landed
+    } else {
+        __builtin_amdgcn_s_waitcnt(kWaitVm(0));
+    }
+    __syncthreads();
+    f16v_t sc[2];
+    s_product(B0{}, sc);
+    // block j uses K buffer j & 1 and V buffer j & 1; the loop is unrolled by
+    // two so every buffer choice is a compile-time constant
+    auto step = [&](int j, auto par) {
+        constexpr int P = decltype(par)::value;
+        using Pn = std::integral_constant<int, P ^ 1>;
+        __builtin_amdgcn_s_waitcnt(kWaitVm(0));
+        __syncthreads();
+        issue_v(j + 1, Pn{});
+        if (j + 2 < nb) issue_k(j + 2, par);
+        f16v_t sn[2];
+        Vec16 pf[4];
+        float alpha;
+        bool rescale = false;
+        softmax(sc, pf, alpha, rescale, k_lo + j * kBN, std::false_type{});
+        s_product(Pn{}, sn);
+        rescale_o(alpha, rescale);
+        pv_product(par, pf);
+        sc[0] = sn[0];
+        sc[1] = sn[1];
+    };
+    for (int j = 0; j + 1 < nb; j += 2) {
+        step(j, B0{});
+        if (j + 2 < nb) step(j + 1, B1{});
+    }
+    {
+        __builtin_amdgcn_s_waitcnt(kWaitVm(0));
+        __syncthreads();
+        const int kb = k_lo + (nb - 1) * kBN;
+        Vec16 pf[4];
+        float alpha;
+        bool rescale = false;
+        if (kb + kBN > k_hi)
+            softmax(sc, pf, alpha, rescale, kb, std::true_type{});
+        else
+            softmax(sc, pf, alpha, rescale, kb, std::false_type{});
+        rescale_o(alpha, rescale);
+        if ((nb - 1) & 1)
+            pv_product(B1{}, pf);
+        else
+            pv_product(B0{}, pf);
+    }
+    __syncthreads();  // the LDS is reused by the fused epilogue
+
+    const float l_tot = xor32_sum(l_run);  // both halves of the query's keys
+    m_run *= p.scale_log2;                 // to the log2 units of the tree walk's scores
+
+    if constexpr (!FUSED) {
+        // ---- partial state of this split: (m, l, acc / l).  For fp16
+        // inputs the normalised numerator is stored in fp16, which halves the
+        // bytes the merge reads, as the reference's own split pipelines hand
+        // fp16 partial outputs to their merge (scripts/benchmark_micro.py:
+        // 576-592, src/ragged_attn.py:1619); bf16 inputs keep fp32 states.
+        // Element 4 j + e of d-tile dt is dim 32 dt + 8 j + 4 hl + e. ----
+        int64_t qrow;
+        int qh;
+        if (query_of(qrow, qh)) {
+            const int64_t plane = p.total_tokens * (int64_t)p.Hq;
+            const int64_t idx = (int64_t)split * plane + qrow * p.Hq + qh;
+            if (hl == 0) {
+                p.part_m[idx] = m_run;
+                p.part_l[idx] = l_tot;
+            }
+            const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+            const int64_t off = idx * D + 4 * hl;
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) {
+#pragma unroll
+                for (int jj = 0; jj < 4; ++jj) {
+                    const float a = oacc[dt][4 * jj] * inv, b = oacc[dt][4 * jj + 1] * inv;
+                    const float c = oacc[dt][4 * jj + 2] * inv, d = oacc[dt][4 * jj + 3] * inv;
+                    if constexpr (kPartHalf<T>)
+                        *reinterpret_cast<uint2*>((uint16_t*)p.part_acc + off + 32 * dt + 8 * jj) =
+                            make_uint2(MfmaOps<F16>::pack2(a, b), MfmaOps<F16>::pack2(c, d));
+                    else
+                        *reinterpret_cast<float4*>((float*)p.part_acc + off + 32 * dt + 8 * jj) = make_float4(a, b, c, d);
+                }
+            }
+        }
+    } else {
+        // ---- fused epilogue: each wave re-lays its 32 rows in its own LDS
+        // buffer as 4 lanes per query (no other wave reads it, so only the
+        // wave's own LDS order matters), takes m and l by shuffles, and runs
+        // the ancestor walks of its two 16-row blocks with their loads
+        // interleaved ----
+        constexpr int NCH = D / 32;
+        constexpr int C4 = D / 4;  // float4 per staged row; float4 c of row r sits at c ^ (r & 7)
+        uint16_t* wbuf = wave == 0 ? Kb0 : (wave == 1 ? Kb1 : (wave == 2 ? Vb0 : Vb1));
+        float4* Os = reinterpret_cast<float4*>(wbuf);  // [32 rows][C4]
+        static_assert(32 * D * 4 <= BLK * 2, "epilogue staging must fit one K/V buffer");
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj)
+                Os[q32 * C4 + ((8 * dt + 2 * jj + hl) ^ (q32 & 7))] = make_float4(
+                    oacc[dt][4 * jj], oacc[dt][4 * jj + 1], oacc[dt][4 * jj + 2], oacc[dt][4 * jj + 3]);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        const int grp = lane >> 2, j = lane & 3;
+        float acc[kQB][8 * NCH], mw[kQB], lw[kQB];
+        int tokb[kQB], hb[kQB];
+        int64_t qrb[kQB];
+        bool vb[kQB];
+        Vec16 qf4[kQB][NCH];
+#pragma unroll
+        for (int b = 0; b < kQB; ++b) {
+            const int rr = qt * kBM + wave * (16 * kQB) + 16 * b + grp;
+            vb[b] = rr < rows;
+            // a row past the tile's queries walks the tile's first token (valid
+            // memory, ancestors inside the staged ranges) and stores nothing
+            tokb[b] = vb[b] ? divide(rr, p.gdiv) : (qt * kBM) / g;
+            hb[b] = kvh * g + (vb[b] ? rr - tokb[b] * g : 0);
+            qrb[b] = (int64_t)s0 + tokb[b];
+            const int row = 16 * b + grp;
+#pragma unroll
+            for (int i = 0; i < NCH; ++i) {
+                const float4 a0 = Os[row * C4 + ((2 * (j + 4 * i)) ^ (row & 7))];
+                const float4 a1 = Os[row * C4 + ((2 * (j + 4 * i) + 1) ^ (row & 7))];
+                acc[b][8 * i + 0] = a0.x;
+                acc[b][8 * i + 1] = a0.y;
+                acc[b][8 * i + 2] = a0.z;
+                acc[b][8 * i + 3] = a0.w;
+                acc[b][8 * i + 4] = a1.x;
+                acc[b][8 * i + 5] = a1.y;
+                acc[b][8 * i + 6] = a1.z;
+                acc[b][8 * i + 7] = a1.w;
+            }
+            // query 16 b + grp's state is held by lane 16 b + grp of the MFMA layout
+            mw[b] = __shfl(m_run, 16 * b + grp);
+            lw[b] = __shfl(l_tot, 16 * b + grp);
+            if constexpr (WALK != WALK_NONE) load_q4<D, BATCH>(tp, seq, qrb[b], hb[b], j, qf4[b]);
+        }
+        if constexpr (WALK != WALK_NONE) {  // (prefix only: nothing to walk)
+        // Heap parents are monotonic, so walk step t of every token in the
+        // tile's range [tl, th] lies in [par^t(tl), par^t(th)].  When those
+        // ranges (steps 1 ..) total at most 128 rows they are staged once in
+        // LDS, level after level (K rows in Kb0/Kb1, V rows in Vb0/Vb1, 64 rows
+        // per buffer), and the walks read them there; each query's own row
+        // (step 0) comes from global memory.  Otherwise the walks gather every
+        // step from global memory.
+        // (The explicit-parents walk has no such ranges and always gathers.)
+        constexpr int kRowsPerBuf = BLK / D;
+        constexpr int kLdsRows = 2 * kRowsPerBuf;
+        const int tl = (qt * kBM) / g;
+        const int th = (min(qt * kBM + kBM, rows) - 1) / g;
+        int nlev = 0, total = WALK == WALK_HEAP ? 0 : kLdsRows + 1;
+        if constexpr (WALK == WALK_HEAP) {
+            int lo = tl, hi = th;
+            for (int t = 1; t <= tp.max_depth && total <= kLdsRows; ++t) {
+                if (lo == 0 && hi == 0) break;  // past the root every step is a self-loop
+                lo = heap_parent(lo, tp.bdiv);
+                hi = heap_parent(hi, tp.bdiv);
+                total += hi - lo + 1;
+                nlev = t;
+            }
+        }
+        // (DBG: lane 0 of each query's group owns the query's export row)
+        int32_t* dbg[kQB] = {};
+        if constexpr (DBG) {
+#pragma unroll
+            for (int b = 0; b < kQB; ++b) {
+                if (vb[b] && j == 0) {
+                    dbg[b] = tp.dbg_walk + (qrb[b] * tp.Hq + hb[b]) * (tp.max_depth + 1);
+                    for (int i = 0; i <= tp.max_depth; ++i) dbg[b][i] = -1;
+                }
+            }
+        }
+        if (WALK == WALK_HEAP && total <= kLdsRows) {
+            const int64_t kvb = kv_base(tp, seq, s0);
+            const uint16_t* kg = (const uint16_t*)tp.k + (int64_t)kvh * tp.sk_h;
+            const uint16_t* vg = (const uint16_t*)tp.v + (int64_t)kvh * tp.sv_h;
+            auto krow = [&](int slot) { return (slot < kRowsPerBuf ? Kb0 : Kb1) + (slot % kRowsPerBuf) * D; };
+            auto vrow = [&](int slot) { return (slot < kRowsPerBuf ? Vb0 : Vb1) + (slot % kRowsPerBuf) * D; };
+            // step 0 loads go out before the staging
+            Vec16 k0[kQB][NCH], v0[kQB][NCH];
+#pragma unroll
+            for (int b = 0; b < kQB; ++b)
+#pragma unroll
+                for (int i = 0; i < NCH; ++i) {
+                    k0[b][i] = ld16(kg + (kvb + tokb[b]) * tp.sk_t + 8 * j + 32 * i);
+                    v0[b][i] = ld16(vg + (kvb + tokb[b]) * tp.sv_t + 8 * j + 32 * i);
+                }
+            __syncthreads();  // every wave has read its staged O
+            {
+                int lo = tl, hi = th, off = 0;
+                for (int t = 1; t <= nlev; ++t) {
+                    lo = heap_parent(lo, tp.bdiv);
+                    hi = heap_parent(hi, tp.bdiv);
+                    const int sz = hi - lo + 1;
+                    for (int idx = tid; idx < sz * DV; idx += kPrefixThreads) {
+                        const int r = idx / DV, c = idx - r * DV;
+                        const int64_t grow = kvb + lo + r;
+                        st16(krow(off + r) + 8 * c, ld16(kg + grow * tp.sk_t + 8 * c));
+                        st16(vrow(off + r) + 8 * c, ld16(vg + grow * tp.sv_t + 8 * c));
+                        if constexpr (DBG) {
+                            if (c == 0) dbg_slot[off + r] = lo + r;
+                        }
+                    }
+                    off += sz;
+                }
+            }
+            __syncthreads();
+            int32_t cur[kQB], prev[kQB];
+#pragma unroll
+            for (int b = 0; b < kQB; ++b) {
+                float sc = qk4<T, NCH>(qf4[b], k0[b]) * tp.scale_log2;
+                fold_scores<T, NCH, 1>(&sc, &v0[b], mw[b], lw[b], acc[b]);
+                if constexpr (DBG) {
+                    if (dbg[b]) dbg[b][0] = tokb[b];
+                }
+                prev[b] = tokb[b];
+                cur[b] = heap_parent(tokb[b], tp.bdiv);
+            }
+            int lo = tl, hi = th, off = 0;
+            for (int t = 1; t <= nlev; ++t) {
+                lo = heap_parent(lo, tp.bdiv);
+                hi = heap_parent(hi, tp.bdiv);
+#pragma unroll
+                for (int b = 0; b < kQB; ++b) {
+                    const int slot = off + cur[b] - lo;  // inside [off, off + hi - lo] by monotonicity
+                    Vec16 kk[NCH], vv[1][NCH];
+#pragma unroll
+                    for (int i = 0; i < NCH; ++i) {
+                        kk[i] = ld16(krow(slot) + 8 * j + 32 * i);
+                        vv[0][i] = ld16(vrow(slot) + 8 * j + 32 * i);
+                    }
+                    float sc = qk4<T, NCH>(qf4[b], kk) * tp.scale_log2;
+                    sc = cur[b] != prev[b] ? sc : -INFINITY;  // the root's self-loop is not a step
+                    fold_scores<T, NCH, 1>(&sc, vv, mw[b], lw[b], acc[b]);
+                    if constexpr (DBG) {
+                        if (dbg[b]) dbg[b][t] = cur[b] != prev[b] ? dbg_slot[slot] : -1;
+                    }
+                    prev[b] = cur[b];
+                    cur[b] = heap_parent(cur[b], tp.bdiv);
+                }
+                off += hi - lo + 1;
+            }
+        } else {
+            // steps per chunk of each walk: half the single-walk chunk from
+            // D = 64 up (two full chunks in flight spill registers there)
+            constexpr int CH1 = 8 / NCH;
+            constexpr int CHW = D >= 64 ? CH1 / 2 : CH1;
+            using W = Walk4<T, D, WALK, KV_PACKED, CHW, BATCH, DBG>;
+            W w0(tp, seq, s0, n, tokb[0], kvh, j, nullptr, dbg[0]), w1(tp, seq, s0, n, tokb[1], kvh, j, nullptr, dbg[1]);
+            w0.issue();
+            w1.issue();
+            w0.fold(qf4[0], mw[0], lw[0], acc[0]);
+            w1.fold(qf4[1], mw[1], lw[1], acc[1]);
+            for (;;) {
+                const bool a0 = w0.more(), a1 = w1.more();
+                if (!a0 && !a1) break;
+                if (a0) w0.issue();
+                if (a1) w1.issue();
+                if (a0) w0.fold(qf4[0], mw[0], lw[0], acc[0]);
+                if (a1) w1.fold(qf4[1], mw[1], lw[1], acc[1]);
+            }
+        }
+        }
+#pragma unroll
+        for (int b = 0; b < kQB; ++b)
+            if (vb[b]) write_out4<T, D, LSE, BATCH>(tp, seq, qrb[b], hb[b], j, mw[b], lw[b], acc[b]);
+    }
+}
+
+
+// Half-height split kernel: 64-row query tiles, one 16-row column block per
+// wave, v_mfma_f32_16x16x32 products, partial states only.  It serves split
+// calls whose units would leave CUs idle (a decode step of a small tree):
+// half the rows per unit gives twice the units.
+template <typename T, int D, bool BATCH>
+__global__ __launch_bounds__(kPrefixThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefix_half_kernel(
+    PrefixParams p) {
+    constexpr int QB = 1;
     constexpr int kQB = QB;         // (hides the namespace default) column blocks per wave
     constexpr int kBM = 64 * QB;    // query rows per workgroup
     constexpr int NC = D / 32;      // MFMA k-chunks over the head dim
@@ -119,8 +673,6 @@ __global__ __launch_bounds__(kPrefixThreads) __attribute__((amdgpu_waves_per_eu(
     // compiler tells them apart: a read of one buffer does not wait for the
     // LDS-DMA loads in flight into another.
     __shared__ __attribute__((aligned(1024))) uint16_t Kb0[BLK], Kb1[BLK], Vb0[BLK], Vb1[BLK];
-    // DBG only: the node of each row the epilogue stages in LDS
-    __shared__ int32_t dbg_slot[DBG ? 2 * (BLK / D) : 1];
     auto kbuf = [&](auto i) -> uint16_t* {
         if constexpr (decltype(i)::value == 0) return Kb0; else return Kb1;
     };
@@ -432,7 +984,6 @@ __global__ __launch_bounds__(kPrefixThreads) __attribute__((amdgpu_waves_per_eu(
         else
             pv_product(B0{}, pf);
     }
-    __syncthreads();  // the LDS is reused by the fused epilogue
 
     float l_tot[kQB];
 #pragma unroll
@@ -441,7 +992,7 @@ __global__ __launch_bounds__(kPrefixThreads) __attribute__((amdgpu_waves_per_eu(
         m_run[b] *= p.scale_log2;  // to the log2 units of the tree walk's scores
     }
 
-    if constexpr (!FUSED) {
+    {
         // ---- partial state of this split: (m, l, acc / l).  For fp16
         // inputs the normalised numerator is stored in fp16, which halves the
         // bytes the merge reads, as the reference's own split pipelines hand
@@ -472,191 +1023,6 @@ __global__ __launch_bounds__(kPrefixThreads) __attribute__((amdgpu_waves_per_eu(
                                     oacc[b][dt][3] * inv);
             }
         }
-    } else {
-        // ---- fused epilogue: each wave re-lays both of its 16-row blocks in
-        // its own LDS buffer as 4 lanes per query (no other wave reads it, so
-        // only the wave's own LDS order matters), takes m and l by shuffles,
-        // and runs the two ancestor walks with their loads interleaved ----
-        static_assert(kQB == 2, "the epilogue walks two column blocks together");
-        constexpr int NCH = D / 32;
-        constexpr int C4 = D / 4;  // float4 per staged row; float4 c of row r sits at c ^ (r & 7)
-        uint16_t* wbuf = wave == 0 ? Kb0 : (wave == 1 ? Kb1 : (wave == 2 ? Vb0 : Vb1));
-        float4* Os = reinterpret_cast<float4*>(wbuf);  // [kQB * 16 rows][C4]
-        static_assert(kQB * 16 * D * 4 <= BLK * 2, "epilogue staging must fit one K/V buffer");
-#pragma unroll
-        for (int b = 0; b < kQB; ++b) {
-            const int row = 16 * b + l16;
-#pragma unroll
-            for (int dt = 0; dt < ND; ++dt)
-                Os[row * C4 + ((4 * dt + lq) ^ (row & 7))] =
-                    make_float4(oacc[b][dt][0], oacc[b][dt][1], oacc[b][dt][2], oacc[b][dt][3]);
-        }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        const int grp = lane >> 2, j = lane & 3;
-        float acc[kQB][8 * NCH], mw[kQB], lw[kQB];
-        int tokb[kQB], hb[kQB];
-        int64_t qrb[kQB];
-        bool vb[kQB];
-        Vec16 qf4[kQB][NCH];
-#pragma unroll
-        for (int b = 0; b < kQB; ++b) {
-            const int rr = qt * kBM + wave * (16 * kQB) + 16 * b + grp;
-            vb[b] = rr < rows;
-            // a row past the tile's queries walks the tile's first token (valid
-            // memory, ancestors inside the staged ranges) and stores nothing
-            tokb[b] = vb[b] ? divide(rr, p.gdiv) : (qt * kBM) / g;
-            hb[b] = kvh * g + (vb[b] ? rr - tokb[b] * g : 0);
-            qrb[b] = (int64_t)s0 + tokb[b];
-            const int row = 16 * b + grp;
-#pragma unroll
-            for (int i = 0; i < NCH; ++i) {
-                const float4 a0 = Os[row * C4 + ((2 * (j + 4 * i)) ^ (row & 7))];
-                const float4 a1 = Os[row * C4 + ((2 * (j + 4 * i) + 1) ^ (row & 7))];
-                acc[b][8 * i + 0] = a0.x;
-                acc[b][8 * i + 1] = a0.y;
-                acc[b][8 * i + 2] = a0.z;
-                acc[b][8 * i + 3] = a0.w;
-                acc[b][8 * i + 4] = a1.x;
-                acc[b][8 * i + 5] = a1.y;
-                acc[b][8 * i + 6] = a1.z;
-                acc[b][8 * i + 7] = a1.w;
-            }
-            // query grp's state is held by lane grp of the MFMA layout (l16 = grp, lq = 0)
-            mw[b] = __shfl(m_run[b], grp);
-            lw[b] = __shfl(l_tot[b], grp);
-            if constexpr (WALK != WALK_NONE) load_q4<D, BATCH>(tp, seq, qrb[b], hb[b], j, qf4[b]);
-        }
-        if constexpr (WALK != WALK_NONE) {  // (prefix only: nothing to walk)
-        // Heap parents are monotonic, so walk step t of every token in the
-        // tile's range [tl, th] lies in [par^t(tl), par^t(th)].  When those
-        // ranges (steps 1 ..) total at most 128 rows they are staged once in
-        // LDS, level after level (K rows in Kb0/Kb1, V rows in Vb0/Vb1, 64 rows
-        // per buffer), and the walks read them there; each query's own row
-        // (step 0) comes from global memory.  Otherwise the walks gather every
-        // step from global memory.
-        // (The explicit-parents walk has no such ranges and always gathers.)
-        constexpr int kRowsPerBuf = BLK / D;
-        constexpr int kLdsRows = 2 * kRowsPerBuf;
-        const int tl = (qt * kBM) / g;
-        const int th = (min(qt * kBM + kBM, rows) - 1) / g;
-        int nlev = 0, total = WALK == WALK_HEAP ? 0 : kLdsRows + 1;
-        if constexpr (WALK == WALK_HEAP) {
-            int lo = tl, hi = th;
-            for (int t = 1; t <= tp.max_depth && total <= kLdsRows; ++t) {
-                if (lo == 0 && hi == 0) break;  // past the root every step is a self-loop
-                lo = heap_parent(lo, tp.bdiv);
-                hi = heap_parent(hi, tp.bdiv);
-                total += hi - lo + 1;
-                nlev = t;
-            }
-        }
-        // (DBG: lane 0 of each query's group owns the query's export row)
-        int32_t* dbg[kQB] = {};
-        if constexpr (DBG) {
-#pragma unroll
-            for (int b = 0; b < kQB; ++b) {
-                if (vb[b] && j == 0) {
-                    dbg[b] = tp.dbg_walk + (qrb[b] * tp.Hq + hb[b]) * (tp.max_depth + 1);
-                    for (int i = 0; i <= tp.max_depth; ++i) dbg[b][i] = -1;
-                }
-            }
-        }
-        if (WALK == WALK_HEAP && total <= kLdsRows) {
-            const int64_t kvb = kv_base(tp, seq, s0);
-            const uint16_t* kg = (const uint16_t*)tp.k + (int64_t)kvh * tp.sk_h;
-            const uint16_t* vg = (const uint16_t*)tp.v + (int64_t)kvh * tp.sv_h;
-            auto krow = [&](int slot) { return (slot < kRowsPerBuf ? Kb0 : Kb1) + (slot % kRowsPerBuf) * D; };
-            auto vrow = [&](int slot) { return (slot < kRowsPerBuf ? Vb0 : Vb1) + (slot % kRowsPerBuf) * D; };
-            // step 0 loads go out before the staging
-            Vec16 k0[kQB][NCH], v0[kQB][NCH];
-#pragma unroll
-            for (int b = 0; b < kQB; ++b)
-#pragma unroll
-                for (int i = 0; i < NCH; ++i) {
-                    k0[b][i] = ld16(kg + (kvb + tokb[b]) * tp.sk_t + 8 * j + 32 * i);
-                    v0[b][i] = ld16(vg + (kvb + tokb[b]) * tp.sv_t + 8 * j + 32 * i);
-                }
-            __syncthreads();  // every wave has read its staged O
-            {
-                int lo = tl, hi = th, off = 0;
-                for (int t = 1; t <= nlev; ++t) {
-                    lo = heap_parent(lo, tp.bdiv);
-                    hi = heap_parent(hi, tp.bdiv);
-                    const int sz = hi - lo + 1;
-                    for (int idx = tid; idx < sz * DV; idx += kPrefixThreads) {
-                        const int r = idx / DV, c = idx - r * DV;
-                        const int64_t grow = kvb + lo + r;
-                        st16(krow(off + r) + 8 * c, ld16(kg + grow * tp.sk_t + 8 * c));
-                        st16(vrow(off + r) + 8 * c, ld16(vg + grow * tp.sv_t + 8 * c));
-                        if constexpr (DBG) {
-                            if (c == 0) dbg_slot[off + r] = lo + r;
-                        }
-                    }
-                    off += sz;
-                }
-            }
-            __syncthreads();
-            int32_t cur[kQB], prev[kQB];
-#pragma unroll
-            for (int b = 0; b < kQB; ++b) {
-                float sc = qk4<T, NCH>(qf4[b], k0[b]) * tp.scale_log2;
-                fold_scores<T, NCH, 1>(&sc, &v0[b], mw[b], lw[b], acc[b]);
-                if constexpr (DBG) {
-                    if (dbg[b]) dbg[b][0] = tokb[b];
-                }
-                prev[b] = tokb[b];
-                cur[b] = heap_parent(tokb[b], tp.bdiv);
-            }
-            int lo = tl, hi = th, off = 0;
-            for (int t = 1; t <= nlev; ++t) {
-                lo = heap_parent(lo, tp.bdiv);
-                hi = heap_parent(hi, tp.bdiv);
-#pragma unroll
-                for (int b = 0; b < kQB; ++b) {
-                    const int slot = off + cur[b] - lo;  // inside [off, off + hi - lo] by monotonicity
-                    Vec16 kk[NCH], vv[1][NCH];
-#pragma unroll
-                    for (int i = 0; i < NCH; ++i) {
-                        kk[i] = ld16(krow(slot) + 8 * j + 32 * i);
-                        vv[0][i] = ld16(vrow(slot) + 8 * j + 32 * i);
-                    }
-                    float sc = qk4<T, NCH>(qf4[b], kk) * tp.scale_log2;
-                    sc = cur[b] != prev[b] ? sc : -INFINITY;  // the root's self-loop is not a step
-                    fold_scores<T, NCH, 1>(&sc, vv, mw[b], lw[b], acc[b]);
-                    if constexpr (DBG) {
-                        if (dbg[b]) dbg[b][t] = cur[b] != prev[b] ? dbg_slot[slot] : -1;
-                    }
-                    prev[b] = cur[b];
-                    cur[b] = heap_parent(cur[b], tp.bdiv);
-                }
-                off += hi - lo + 1;
-            }
-        } else {
-            // steps per chunk of each walk: half the single-walk chunk from
-            // D = 64 up (two full chunks in flight spill registers there)
-            constexpr int CH1 = 8 / NCH;
-            constexpr int CHW = D >= 64 ? CH1 / 2 : CH1;
-            using W = Walk4<T, D, WALK, KV_PACKED, CHW, BATCH, DBG>;
-            W w0(tp, seq, s0, n, tokb[0], kvh, j, nullptr, dbg[0]), w1(tp, seq, s0, n, tokb[1], kvh, j, nullptr, dbg[1]);
-            w0.issue();
-            w1.issue();
-            w0.fold(qf4[0], mw[0], lw[0], acc[0]);
-            w1.fold(qf4[1], mw[1], lw[1], acc[1]);
-            for (;;) {
-                const bool a0 = w0.more(), a1 = w1.more();
-                if (!a0 && !a1) break;
-                if (a0) w0.issue();
-                if (a1) w1.issue();
-                if (a0) w0.fold(qf4[0], mw[0], lw[0], acc[0]);
-                if (a1) w1.fold(qf4[1], mw[1], lw[1], acc[1]);
-            }
-        }
-        }
-#pragma unroll
-        for (int b = 0; b < kQB; ++b)
-            if (vb[b]) write_out4<T, D, LSE, BATCH>(tp, seq, qrb[b], hb[b], j, mw[b], lw[b], acc[b]);
     }
 }
 
@@ -780,8 +1146,7 @@ static void launch_prefix_b(const PrefixParams& pp, const TreeParams& tp, bool f
         }
     }
     if (!fused && half)
-        hipLaunchKernelGGL((prefix_attn_kernel<T, D, false, false, WALK_HEAP, BATCH, false, 1>), g, b, 0, st, pp,
-                           tp);
+        hipLaunchKernelGGL((prefix_half_kernel<T, D, BATCH>), g, b, 0, st, pp);
     else if (!fused)
         hipLaunchKernelGGL((prefix_attn_kernel<T, D, false, false, WALK_HEAP, BATCH>), g, b, 0, st, pp, tp);
     else if (walk == WALK_NONE && tp.lse)

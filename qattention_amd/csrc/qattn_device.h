@@ -188,6 +188,43 @@ struct MfmaOps<BF16> {
     static __device__ __forceinline__ float hi(uint32_t w) { return __builtin_bit_cast(float, w & 0xffff0000u); }
 };
 
+// ---------------------------------------------------------------------------
+// v_mfma_f32_32x32x16_{f16,bf16} (gfx950; lane l, h = l / 32, c = l % 32;
+// checked element by element on the GPU with exact small integers):
+//   A (32 x 16): lane holds A[c][8h .. 8h+7]      (one 16-byte vector)
+//   B (16 x 32): lane holds B[8h .. 8h+7][c]
+//   D (32 x 32): lane holds D[8(r/4) + 4h + r%4][c] in element r, r = 0..15
+// One 32x32x16 product is twice the FLOPs of a 16x16x32 one; a stream of
+// them with this prefix kernel's softmax mix and LDS operand reads sustained
+// 66% of the fp16 peak at 2 waves per SIMD, against 33% for 16x16x32.
+// ---------------------------------------------------------------------------
+typedef float f16v_t __attribute__((ext_vector_type(16)));
+
+template <typename T>
+__device__ __forceinline__ f16v_t mma32(const Vec16& a, const Vec16& b, f16v_t c);
+template <>
+__device__ __forceinline__ f16v_t mma32<F16>(const Vec16& a, const Vec16& b, f16v_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(h8_t, a), __builtin_bit_cast(h8_t, b), c, 0, 0,
+                                                  0);
+}
+template <>
+__device__ __forceinline__ f16v_t mma32<BF16>(const Vec16& a, const Vec16& b, f16v_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(b8_t, a), __builtin_bit_cast(b8_t, b), c, 0, 0,
+                                                   0);
+}
+
+// Reductions over the lane pair l, l ^ 32 (one column of a 32x32 MFMA output).
+__device__ __forceinline__ float xor32_max(float x) {
+    auto b = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, x), __builtin_bit_cast(uint32_t, x),
+                                              false, false);
+    return fmaxf(__builtin_bit_cast(float, (uint32_t)b[0]), __builtin_bit_cast(float, (uint32_t)b[1]));
+}
+__device__ __forceinline__ float xor32_sum(float x) {
+    auto b = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, x), __builtin_bit_cast(uint32_t, x),
+                                              false, false);
+    return __builtin_bit_cast(float, (uint32_t)b[0]) + __builtin_bit_cast(float, (uint32_t)b[1]);
+}
+
 // Prefix split states store each query's numerator / l, a convex
 // combination of V rows: in fp16 for fp16 inputs (it fits fp16's range, and
 // half the bytes of fp32 is half of what the split merge reads), in fp32 for
