@@ -258,8 +258,13 @@ def test_cfg5_every_sequence():
     """B=16, L=2048, b=8 d=4 (N=4681), H=32, sigma=0.5: the GPU runs the full
     configuration; the padded-SDPA oracle (fp32, MATH) checks every token of
     every sequence -- each sequence's last partial 128-row tile included --
-    on two heads per sequence (heads 2s and 2s+1, so the 16 sequences cover
-    all 32 heads), and every output is finite."""
+    on four heads per sequence (heads 4s .. 4s+3 mod 32, so every head is
+    checked on two sequences), and every output is finite.  Every token of
+    every head is then checked against the reference's three-step pipeline
+    run through other kernels (scripts/benchmark_micro.py:568-593): the
+    prefix-only pass, the tree pass with LSE on the subtree kernel and
+    fused_lse_merge -- the FA2 merge identity, within the two extra fp16
+    roundings of O_pre and O_tree."""
     ra = _ra()
     B, b, d, H, D, L = 16, 8, 4, 32, 128, 2048
     N = num_tree_nodes(b, d)
@@ -273,12 +278,25 @@ def test_cfg5_every_sequence():
     m = otree.tree_attention_mask(b, d)
     for s in range(B):
         rows = slice(s * N, (s + 1) * N)
-        heads = slice(2 * s, 2 * s + 2)
-        outs, lses = sdpa.padded_sdpa([Q[rows, heads]], [K[rows, heads]], [V[rows, heads]], [m],
-                                      [Kp[s, :, heads]], [Vp[s, :, heads]], return_lse=True)
-        check_fp16(O[rows, heads].double().numpy(), outs[0].double().numpy(), f"cfg5 seq {s}")
-        assert float((LSE[rows, heads] - lses[0]).abs().max()) <= 1e-4, f"cfg5 LSE seq {s}"
-        say("cfg5 seq", s, "ok")
+        heads = [(4 * s + i) % H for i in range(4)]
+        outs, lses = sdpa.padded_sdpa([Q[rows][:, heads]], [K[rows][:, heads]], [V[rows][:, heads]], [m],
+                                      [Kp[s][:, heads]], [Vp[s][:, heads]], return_lse=True)
+        check_fp16(O[rows][:, heads].double().numpy(), outs[0].double().numpy(), f"cfg5 seq {s}")
+        assert float((LSE[rows][:, heads] - lses[0]).abs().max()) <= 1e-4, f"cfg5 LSE seq {s}"
+        say("cfg5 seq", s, "heads", heads, "ok")
+    # every token and head: the pipeline of separate kernels
+    Qd, Kd, Vd, Kpd, Vpd = Q.to(DEV), K.to(DEV), V.to(DEV), Kp.to(DEV), Vp.to(DEV)
+    o_p, lse_p = ra.prefix_attention(Qd, Kpd, Vpd, cu, max_seqlen=N)
+    o_t, lse_t = ra.ragged_attention_with_lse(Qd, Kd, Vd, cu, b, d, max_seqlen=N)
+    to_bhn = lambda x: x.view(B, N, H, -1).permute(0, 2, 1, 3)
+    merged = ra.fused_lse_merge(lse_p.view(B, N, H).permute(0, 2, 1), lse_t.view(B, N, H).permute(0, 2, 1),
+                                to_bhn(o_p), to_bhn(o_t))
+    merged = merged.permute(0, 2, 1, 3).reshape(B * N, H, D).float().cpu()
+    err = float((merged - O.float()).abs().max())
+    say("cfg5 all heads vs the prefix + tree + merge pipeline: max abs", err)
+    assert err <= 4e-3, f"cfg5 vs pipeline: {err:.3e}"
+    lse_m = torch.logaddexp(lse_p, lse_t).cpu()
+    assert float((lse_m - LSE).abs().max()) <= 1e-4
 
 
 @pytest.mark.parametrize("num_splits", [0, 1])
