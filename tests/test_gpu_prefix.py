@@ -299,13 +299,15 @@ def test_cfg5_every_sequence():
     assert float((lse_m - LSE).abs().max()) <= 1e-4
 
 
-@pytest.mark.parametrize("num_splits", [0, 1])
+@pytest.mark.parametrize("num_splits", [0, 1, 24])
 def test_prefix_graph_capture_replay(num_splits):
     """ragged_attention_prefix records into a HIP graph (device cu_seqlens,
     max_seqlen given, workspace from the caching allocator) and every replay
     reproduces the eager O and LSE, with eager work between replays.  Split
-    count 0 picks several splits (prefix kernel + merge/walk kernel), 1 forces
-    the single-split path with the walk fused into the prefix kernel."""
+    count 0 picks 8 splits of half-height tiles (prefix kernel + merge/walk
+    kernel), 24 gives 288 full-height split units (the 128-row tile kernel +
+    merge/walk kernel), 1 forces the single-split path with the walk fused
+    into the prefix kernel."""
     ra = _ra()
     B, b, d, Hq, Hkv, D, L = 2, 4, 3, 8, 2, 128, 1500
     N = num_tree_nodes(b, d)
@@ -335,6 +337,36 @@ def test_prefix_graph_capture_replay(num_splits):
     o_ref, lse_ref, _ = oracle_tree(Q, K, V, cu, b, d, Kp=Kp, Vp=Vp)
     check_fp16(o_eager.double().cpu().numpy(), o_ref, "prefix graph")
     assert np.abs(lse_eager.double().cpu().numpy() - lse_ref).max() <= 1e-4
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_prefix_split_states_repeated_calls(dtype):
+    """Six split calls back to back on different inputs (384 full-height
+    split units: 2 sequences x 8 kv heads x 3 query tiles x 8 splits), no
+    synchronisation between them, each call's split states written where the
+    previous call's merge just read them (the caching allocator hands the
+    same workspace block back): every output and LSE against the oracle.
+    bf16 keeps fp32 states, fp16 fp16 numerators."""
+    ra = _ra()
+    lens, Hq, Hkv, D, L, b, md = [85, 85], 32, 8, 128, 1024, 4, 3
+    cases, outs = [], []
+    for i in range(6):
+        Q, K, V, cu = make_inputs(lens, Hq, D, 700 + i, dtype=dtype, Hkv=Hkv)
+        Kp, Vp = _prefix(len(lens), L, Hkv, D, 800 + i, dtype=dtype)
+        cases.append((Q, K, V, cu, Kp, Vp))
+        outs.append(ra.ragged_attention_prefix(Q.to(DEV), K.to(DEV), V.to(DEV), cu, Kp.to(DEV), Vp.to(DEV), b, md,
+                                               return_lse=True))
+    torch.cuda.synchronize()
+    for i, ((Q, K, V, cu, Kp, Vp), (O, LSE)) in enumerate(zip(cases, outs)):
+        say("repeated split call", i, dtype)
+        o_ref, lse_ref, _ = oracle_tree(Q, K, V, cu, b, md, Kp=Kp, Vp=Vp)
+        o = O.double().cpu().numpy()
+        if dtype == torch.float16:
+            check_fp16(o, o_ref, f"call {i}")
+            assert np.abs(LSE.double().cpu().numpy() - lse_ref).max() <= 1e-4, f"call {i}: LSE"
+        else:
+            check_bf16(o, o_ref, f"call {i}")
+            assert np.abs(LSE.double().cpu().numpy() - lse_ref).max() <= 2e-3, f"call {i}: LSE"
 
 
 @pytest.mark.parametrize("b,d,D,Hq,Hkv", [(2, 9, 128, 4, 4), (2, 8, 64, 8, 2), (3, 6, 128, 2, 2), (8, 3, 128, 4, 4)])
