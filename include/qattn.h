@@ -220,9 +220,9 @@ int qattn_debug_walk(int32_t *out);
  * kernel addresses a 64-key block with 32-bit byte offsets.  Tree key/value row of local ancestor x of sequence
  * s is  tree_seq_stride ? s*tree_seq_stride + tree_row0 + x : cu_seqlens[s] + x
  * (the reference hybrid layout [B*(L+N), H, D] is tree_seq_stride = L+N,
- * tree_row0 = L).  The prefix is computed with v_mfma_f32_16x16x32 in splits
- * along the prefix; the split states are merged into the ancestor walk, which
- * normalises once.  workspace (device, 256-byte aligned, at least
+ * tree_row0 = L).  The prefix is computed with v_mfma_f32_32x32x16 products
+ * (16x16x32 for half-height split tiles) in splits along the prefix; the
+ * split states are merged into the ancestor walk, which normalises once.  workspace (device, 256-byte aligned, at least
  * qattn_prefix_workspace_bytes() bytes for the same sizes and num_splits)
  * holds the split states; num_splits 0 picks a split count for 256 CUs.
  * prefix_len 0 reduces to qattn_tree_fwd (workspace unused).

@@ -4,24 +4,26 @@
 //
 // Work unit: (sequence, kv head, query tile of 128 rows, prefix split).  The
 // rows of a tile are (token, q head) pairs of ONE kv head's GQA group, so a
-// K/V block staged in LDS serves every q head that reads it (no repeat_kv).
-// Each of the 4 waves owns 32 rows as two 16-column blocks and computes, per
-// 64-key block,
-//   S^T = K Q^T      32 x v_mfma_f32_16x16x32_{f16,bf16}   (D = 128)
-//   O^T += V^T P^T   32 x v_mfma_f32_16x16x32_{f16,bf16}
-// Every K and V^T operand read from LDS feeds both column blocks.  Computing
-// S transposed puts one query per lane column, so the softmax statistics need
-// only a 4-lane (xor 16, xor 32) reduction, and the S^T output registers are
-// directly the P^T operand of the next product (keys are permuted the same way
-// in P^T and in the LDS copy of V^T).
+// K/V block staged in LDS (by LDS-DMA, global_load_lds_dwordx4) serves every
+// q head that reads it (no repeat_kv).  Each of the 4 waves owns 32 rows as
+// the N dimension of v_mfma_f32_32x32x16_{f16,bf16} products and computes,
+// per 64-key block,
+//   S^T = K Q^T      2 key tiles x D/16 k-steps   (16 products at D = 128)
+//   O^T += V^T P^T   4 16-key steps x D/32 d-tiles (16 products at D = 128)
+// Computing S transposed puts one query per lane column (lanes l and l + 32
+// split its keys), so the softmax statistics need one xor-32 exchange, and
+// the S^T output registers are directly the P^T operand of the next product
+// (keys are permuted the same way in P^T and in the V^T operand reads).
 //
 // Two ways to finish:
-//  * several prefix splits: each split writes its unnormalised state
-//    (m, l, acc) to a caller workspace and the tree kernels (tree_attn.hip)
-//    merge the splits, walk the ancestors and normalise;
+//  * several prefix splits: each split writes its state (m, l, acc / l) to a
+//    caller workspace and the tree kernels (tree_attn.hip) merge the splits,
+//    walk the ancestors and normalise;
 //  * one split (enough query tiles to fill the GPU): the epilogue hands the
-//    state to the ancestor walk in the same workgroup (gather_walk4), which
-//    normalises and stores O -- no partial state leaves the chip.
+//    state to the ancestor walk in the same workgroup, which normalises and
+//    stores O -- no partial state leaves the chip.
+// Split calls with fewer units than CUs use prefix_half_kernel instead
+// (64-row tiles of 16-row v_mfma_f32_16x16x32 column blocks, twice the units).
 #include <algorithm>
 #include <mutex>
 

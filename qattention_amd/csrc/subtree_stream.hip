@@ -7,12 +7,15 @@
 // band; make_subtree_plan in tree_attn.hip).  Every K/V row of a tile is read
 // from HBM once per kv head, and every ancestor read is an LDS read.
 //
-// Pipeline: each workgroup is persistent and walks tiles w, w + gridDim.x,
-// ...  Right after tile i is written to LDS, the workgroup issues the global
-// loads of tile i+1 (its K and V rows and the Q rows of its queries) into
-// registers and then computes tile i from LDS, so HBM sees a steady stream of
-// requests.  With a grid that is a multiple of the tile count a workgroup
-// keeps one tile index, and its level table and load addresses are reused.
+// Pipeline: each workgroup is persistent.  Right after tile i is written to
+// LDS, the workgroup issues the global loads of tile i+1 (its K and V rows and
+// the Q rows of its queries) into registers and then computes tile i from
+// LDS, so HBM sees a steady stream of requests.  The workgroups of a group
+// share one tile index (so a workgroup keeps its level table and load
+// addresses) and take that index's (sequence, kv head) items from the group's
+// atomic counter, one item ahead; without a counter slot (see sched_counters)
+// workgroup j of a group takes items j, j + n, j + 2n, ... of its n-workgroup
+// group instead.
 //
 // Compute, on the matrix cores: a tile holds at most 48 (D = 128) or 64 K/V
 // rows and as many queries, so attention over the tile is three small dense
