@@ -511,7 +511,8 @@ def main():
     ap.add_argument("--algo", default="auto", choices=["auto", "gather", "subtree"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true",
-                    help="cfg2 only: skip the extra timings (cfg3, cfg4 verify / prefix-only, HBM ceiling)")
+                    help="cfg2 only: skip the extra timings (cfg3, cfg4 verify / prefix-only, the EAGLE-3 "
+                         "step, cfg5, the reference's published micro shapes, HBM ceiling)")
     ap.add_argument("--sets", type=int, default=0, help="rotating input sets (0: see n_sets)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain MIB-MiB device copy (counter calibration) and exit")
